@@ -1,0 +1,293 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused GGUF SoA dequantize + GEMV on one MI355X.
+
+Headline (the JSON line's `value`): HBM GB/s of the Q5_0 GEMV sweep over the
+StarCoder2-8B decoder linears at batch (beam) 2: fused qkv 5632x4608, o_proj
+4608x4608, c_fc 18432x4608, c_proj 4608x18432 and lm_head 49152x4608. One step
+is one pass over the five matrices (one GEMV each); `value` = algorithmic
+bytes per step / time per step, where algorithmic bytes = packed weights +
+scales + fp16 x + fp16 y + fp16 bias.
+
+Measurement: seeded synthetic weights resident in HBM. Every matrix exists in
+8 distinct copies (>= 2.4 GB per pass rotation), so each launch reads weights
+that the 256 MB Infinity Cache no longer holds; the timed region replays a HIP
+graph of 8 passes, bracketed by HIP events on the launch stream and device
+synchronization. The `roofline` object is for the dominant launch (lm_head),
+timed the same way in its own graph. `sweep` holds every GEMV configuration
+(1B Q4_0 shapes, 8B Q5_0 shapes, 8192x2048 Q8_0, the beam-width sweep),
+each as the median of 5 trials over >= 1 GiB of rotating copies.
+`cpu_baseline` times the reference's CPU path (tiled fp32 dequantize +
+F.linear, restated in oracle/) on the host cores for one pass of the same
+step.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+import __graft_entry__  # noqa: E402
+
+__graft_entry__.register_package()
+import starvector_amd._native as native  # noqa: E402
+from starvector_amd.quantization import BLOCK_BYTES  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "quant GEMV HBM GB/s (% of peak) at 8B shapes; 8B beam-2 decode tokens/s"
+STEP_SHAPES = [  # (name, n, k, has_bias) of the 8B decoder step, Q5_0, batch 2
+    ("qkv", 5632, 4608, True), ("o_proj", 4608, 4608, True), ("c_fc", 18432, 4608, True),
+    ("c_proj", 4608, 18432, True), ("lm_head", 49152, 4608, False)]
+STEP_QTYPE, STEP_M, COPIES = "Q5_0", 2, 8
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(qtype, n, k, m, bias):
+    return n * k // 32 * BLOCK_BYTES[qtype] + 2 * m * k + 2 * m * n + (2 * n if bias else 0)
+
+
+class Pool:
+    """Distinct weight copies carved from two large seeded device buffers."""
+
+    def __init__(self, dev, q_bytes, s_bytes, seed=1234):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.q = torch.randint(0, 256, (q_bytes,), dtype=torch.uint8, device=dev, generator=g)
+        d = torch.rand(s_bytes // 2, device=dev, generator=g) * (2e-2 - 1e-3) + 1e-3
+        self.s = d.half().view(torch.uint8)
+        self.dev = dev
+        self.reset()
+
+    def reset(self):
+        """Start carving from the beginning of the pool again."""
+        self.q_cursor = self.s_cursor = 0
+
+    def copies(self, qtype, n, k, count):
+        """`count` copies at pool regions disjoint from every copy taken since
+        the last reset()."""
+        blocks = n * k // 32
+        qb = blocks * (BLOCK_BYTES[qtype] - 2)
+        sb = blocks * 2
+        align = lambda v: (v + 255) // 256 * 256
+        out = []
+        for i in range(count):
+            qo, so = self.q_cursor, self.s_cursor
+            self.q_cursor += align(qb)
+            self.s_cursor += align(sb)
+            if qo + qb > self.q.numel() or so + sb > self.s.numel():
+                raise ValueError("pool too small")
+            q = self.q[qo:qo + qb]
+            if qtype == "Q8_0":  # keep codes in [-127, 127] as the benchmark specifies
+                q = q.clone()
+                q[q == 0x80] = 0x81
+            out.append((q, self.s[so:so + sb].view(torch.float16)))
+        return out
+
+
+def copies_for(nbytes, cap_bytes):
+    return max(2, min(int(math.ceil(2**30 / nbytes)), cap_bytes // nbytes))
+
+
+def make_call(x, q, s, y, qtype, bias):
+    return lambda: native.gemv(x, q, s.view(torch.uint8), y, qtype, bias)
+
+
+def capture(fns, stream):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        for f in fns:  # warm-up outside capture
+            f()
+        stream.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for f in fns:
+                f()
+    return g
+
+
+def time_graph(graph, stream, replays):
+    """Milliseconds per replay, HIP events on the launch stream."""
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):  # replay() launches on the current stream
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        stop.record(stream)
+    stop.synchronize()
+    return start.elapsed_time(stop) / replays
+
+
+def gemv_case(pool, dev, stream, qtype, n, k, m, bias, trials=5, replays=3):
+    """Median µs per launch over >= 1 GiB of rotating copies."""
+    nbytes = algorithmic_bytes(qtype, n, k, m, bias)
+    count = copies_for(n * k // 32 * BLOCK_BYTES[qtype], pool.q.numel() // 2)
+    pool.reset()
+    cps = pool.copies(qtype, n, k, count)
+    gen = torch.Generator(device=dev).manual_seed(n + k + m)
+    x = torch.randn((m, k), device=dev, generator=gen).half()
+    b = torch.randn(n, device=dev, generator=gen).half() if bias else None
+    y = torch.empty((m, n), dtype=torch.float16, device=dev)
+    graph = capture([make_call(x, q, s, y, qtype, b) for q, s in cps], stream)
+    time_graph(graph, stream, 1)
+    ms = [time_graph(graph, stream, replays) / count for _ in range(trials)]
+    us = statistics.median(ms) * 1e3
+    del graph
+    return {"qtype": qtype, "n": n, "k": k, "m": m, "bias": bias, "copies": count,
+            "us": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "bytes": nbytes}
+
+
+def sweep_cases():
+    cases = [("cfg1", "Q8_0", 8192, 2048, 1, True)]
+    for n, k in ((2304, 2048), (2048, 2048), (8192, 2048), (2048, 8192), (49152, 2048)):
+        for m in (1, 2):
+            cases.append(("cfg2", "Q4_0", n, k, m, n != 49152))
+    for name, n, k, bias in STEP_SHAPES:
+        cases.append(("cfg3", "Q5_0", n, k, 2, bias))
+    for qtype in ("Q4_0", "Q5_0", "Q8_0"):
+        for n, k, bias in ((18432, 4608, True), (49152, 4608, False)):
+            for m in (1, 2, 4, 8):
+                cases.append(("cfg4", qtype, n, k, m, bias))
+    return cases
+
+
+def cpu_baseline(seconds_budget=20.0):
+    """The reference's CPU path (tiled fp32 dequantize + F.linear), restated
+    in oracle/, for one pass of the step at batch 2, timed on this host."""
+    from oracle import soa_oracle as orc
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    total_bytes, elapsed = 0, 0.0
+    per = []
+    for name, n, k, bias in STEP_SHAPES:
+        q, s = orc.synthetic_soa(STEP_QTYPE, n, k, seed=n)
+        qt, st = torch.from_numpy(q), torch.from_numpy(s)
+        x = torch.randn(STEP_M, k)
+        b = torch.randn(n) if bias else None
+        orc.tiled_linear_cpu(x, qt, st, STEP_QTYPE, n, k, b)  # warm-up
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            orc.tiled_linear_cpu(x, qt, st, STEP_QTYPE, n, k, b)
+            runs.append(time.perf_counter() - t0)
+        t = statistics.median(runs)
+        per.append({"shape": f"{name} {n}x{k}", "ms": round(t * 1e3, 2)})
+        total_bytes += algorithmic_bytes(STEP_QTYPE, n, k, STEP_M, bias)
+        elapsed += t
+    return {"value": round(total_bytes / elapsed / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": "one pass of the Q5_0 batch-2 8B step (5 GEMVs) through the reference's "
+                      "CPU path (tiled fp32 dequantize + F.linear), median of 3",
+            "ms_per_step": round(elapsed * 1e3, 1), "per_shape": per}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--quick", action="store_true", help="skip the sweep and CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path runs on one GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+    dev = torch.device("cuda:0")
+    native.load()
+    stream = torch.cuda.Stream(dev)
+    log(f"device: {torch.cuda.get_device_name(dev)}")
+
+    # --- headline step: 8 passes over the 5 matrices, distinct copies -------
+    pool = Pool(dev, q_bytes=3 * 2**30, s_bytes=2**29)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    calls, step_bytes, head = [], 0, None
+    per_shape = {name: [] for name, *_ in STEP_SHAPES}
+    xs = {k: torch.randn((STEP_M, k), device=dev, generator=gen).half() for k in (4608, 18432)}
+    for name, n, k, bias in STEP_SHAPES:
+        cps = pool.copies(STEP_QTYPE, n, k, COPIES)
+        b = torch.randn(n, device=dev, generator=gen).half() if bias else None
+        y = torch.empty((STEP_M, n), dtype=torch.float16, device=dev)
+        per_shape[name] = [make_call(xs[k], q, s, y, STEP_QTYPE, b) for q, s in cps]
+        step_bytes += algorithmic_bytes(STEP_QTYPE, n, k, STEP_M, bias)
+    for i in range(COPIES):
+        for name, *_ in STEP_SHAPES:
+            calls.append(per_shape[name][i])
+    graph = capture(calls, stream)
+    warm_replays = max(1, args.warmup // COPIES)
+    time_graph(graph, stream, warm_replays)
+    replays = max(1, args.steps // COPIES)
+    steps = replays * COPIES
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms_replay = time_graph(graph, stream, replays)
+    wall = time.perf_counter() - t0
+    ms_step = ms_replay / COPIES
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"step: {ms_step * 1e3:.1f} us/step, {value:.1f} GB/s ({value / PEAK_HBM_GBS:.1%} of 8 TB/s), "
+        f"wall {wall:.3f} s for {steps} steps")
+    del graph
+
+    # --- dominant launch: lm_head, own graph over its 8 copies -------------
+    hname, hn, hk, hbias = STEP_SHAPES[-1]
+    hgraph = capture(per_shape[hname], stream)
+    time_graph(hgraph, stream, 2)
+    head_ms = statistics.median(time_graph(hgraph, stream, 5) / COPIES for _ in range(5))
+    head_bytes = algorithmic_bytes(STEP_QTYPE, hn, hk, STEP_M, hbias)
+    achieved = head_bytes / (head_ms * 1e-3) / 1e9
+    del hgraph
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": f"svq gemv_kernel {STEP_QTYPE} M={STEP_M} lm_head {hn}x{hk}",
+                "us_per_launch": round(head_ms * 1e3, 2), "bytes_per_launch": head_bytes}
+    log(f"lm_head: {head_ms * 1e3:.2f} us, {achieved:.1f} GB/s")
+
+    sweep = []
+    if not args.quick:
+        for cfg, qtype, n, k, m, bias in sweep_cases():
+            r = gemv_case(pool, dev, stream, qtype, n, k, m, bias)
+            r["config"] = cfg
+            sweep.append(r)
+            log(f"{cfg} {qtype} {n}x{k} M={m}: {r['us']:.2f} us {r['gbs']:.0f} GB/s ({r['frac']:.1%})")
+
+    cpu = None
+    if not args.quick and not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline()
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": steps, "warmup": warm_replays * COPIES, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded Q5_0 blocks: uniform codes, fp16 scales U[1e-3,2e-2]; fp16 x ~ N(0,1))",
+        "config": {"workload": "Q5_0 GEMV sweep over the StarCoder2-8B decoder linears, batch 2 "
+                               "(qkv 5632x4608, o_proj 4608x4608, c_fc 18432x4608, c_proj 4608x18432, "
+                               "lm_head 49152x4608)",
+                   "batch": STEP_M, "bytes_per_step": step_bytes,
+                   "frac_of_peak": round(value / PEAK_HBM_GBS, 4), "weight_copies": COPIES},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

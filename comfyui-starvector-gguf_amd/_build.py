@@ -1,0 +1,66 @@
+"""Compile libsvq.so (the gfx950 HIP kernels + C ABI) in-tree with hipcc.
+
+Each .hip source under csrc/ becomes an object in _obj/ (compiled in
+parallel), then the objects are linked into libsvq.so next to this file. The
+library is always rebuilt when this runs; callers that only need it loaded use
+`_native.load()`.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+OBJ_DIR = PKG_DIR / "_obj"
+LIB_PATH = PKG_DIR / "libsvq.so"
+INCLUDE_DIR = PKG_DIR.parent / "include"
+
+ARCH = "gfx950"
+# Packed FP32 instructions are disabled for all device code: hipcc would
+# otherwise form v_pk_{add,mul,fma}_f32 from ordinary float code.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+                "-Wall", "-Wno-unused-function", f"-I{INCLUDE_DIR}"]
+
+
+def hipcc() -> str:
+    path = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError(f"hipcc not found (looked for {path})")
+    return path
+
+
+def _compile(src: Path) -> Path:
+    obj = OBJ_DIR / (src.stem + ".o")
+    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
+    return obj
+
+
+def build_library(jobs: int | None = None) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link libsvq.so; returns its path."""
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    OBJ_DIR.mkdir(exist_ok=True)
+    workers = jobs or min(len(sources), os.cpu_count() or 1, 8)
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        objects = list(pool.map(_compile, sources))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+           *map(str, objects)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link of libsvq.so failed:\n{proc.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library())

@@ -1,0 +1,167 @@
+// SoA dequantization for gfx950: every weight is the exact fp32 product of
+// its signed integer code and its block's fp16 scale, then rounded to the
+// output type, as `dequantize_soa` computes it (quantization.py:93-105).
+// One thread decodes one unit (16 or 20 payload bytes) and writes its 16 or
+// 32 outputs as contiguous 16-byte stores. The row-gather variant serves
+// `GGUFEmbedding.forward` (quantization.py:421-446) without index_select
+// copies.
+#include "svq_device.h"
+#include "svq_launch.h"
+
+namespace svq {
+
+constexpr int kDqThreads = 256;
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t b = __builtin_bit_cast(uint32_t, f);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // NaN, as torch
+  b += 0x7fffu + ((b >> 16) & 1u);
+  return (uint16_t)(b >> 16);
+}
+
+template <int OUT, int NV>
+__device__ __forceinline__ void store_values(void* out, int64_t first,
+                                             const float (&v)[NV]) {
+  if constexpr (OUT == 0) {
+    u32x4* o = reinterpret_cast<u32x4*>(reinterpret_cast<float*>(out) + first);
+#pragma unroll
+    for (int i = 0; i < NV / 4; ++i)
+      o[i] = u32x4{__builtin_bit_cast(uint32_t, v[4 * i]),
+                   __builtin_bit_cast(uint32_t, v[4 * i + 1]),
+                   __builtin_bit_cast(uint32_t, v[4 * i + 2]),
+                   __builtin_bit_cast(uint32_t, v[4 * i + 3])};
+  } else {
+    uint16_t h[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      h[i] = OUT == 1 ? __builtin_bit_cast(uint16_t, (_Float16)v[i])
+                      : f32_to_bf16_rne(v[i]);
+    u32x4* o = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(out) + first);
+#pragma unroll
+    for (int i = 0; i < NV / 8; ++i)
+      o[i] = u32x4{h[8 * i] | ((uint32_t)h[8 * i + 1] << 16),
+                   h[8 * i + 2] | ((uint32_t)h[8 * i + 3] << 16),
+                   h[8 * i + 4] | ((uint32_t)h[8 * i + 5] << 16),
+                   h[8 * i + 6] | ((uint32_t)h[8 * i + 7] << 16)};
+  }
+}
+
+// Decode unit `unit` (global unit index) into fp32 values.
+template <int QT>
+__device__ __forceinline__ void decode_unit(const uint8_t* q, const uint16_t* s,
+                                            int64_t unit,
+                                            float (&v)[QTraits<QT>::kUnitWeights]) {
+  using T = QTraits<QT>;
+  uint32_t w[T::kWords];
+  load_unit<QT>(q + unit * T::kUnitBytes, w);
+  const float d = half_bits_to_float(s[unit / T::kUnitsPerBlock]);
+  int c[T::kUnitWeights];
+  unit_codes<QT>(w, c);
+#pragma unroll
+  for (int j = 0; j < T::kUnitWeights; ++j) v[j] = (float)c[j] * d;
+}
+
+template <int QT, int OUT>
+__global__ __launch_bounds__(kDqThreads) void dequant_kernel(
+    const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
+    void* __restrict__ out, int64_t nunits) {
+  using T = QTraits<QT>;
+  const int64_t unit = (int64_t)blockIdx.x * kDqThreads + threadIdx.x;
+  if (unit >= nunits) return;
+  float v[T::kUnitWeights];
+  decode_unit<QT>(q, s, unit, v);
+  store_values<OUT>(out, unit * T::kUnitWeights, v);
+}
+
+template <int QT, int OUT>
+__global__ __launch_bounds__(kDqThreads) void dequant_rows_kernel(
+    const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
+    const int64_t* __restrict__ ids, int64_t nids, int64_t nrows,
+    int units_per_row, void* __restrict__ out) {
+  using T = QTraits<QT>;
+  const int64_t t = (int64_t)blockIdx.x * kDqThreads + threadIdx.x;
+  if (t >= nids * units_per_row) return;
+  const int64_t i = t / units_per_row;
+  const int64_t ur = t - i * units_per_row;
+  const int64_t id = ids[i];
+  float v[T::kUnitWeights];
+  if (id < 0 || id >= nrows) {
+#pragma unroll
+    for (int j = 0; j < T::kUnitWeights; ++j) v[j] = __builtin_nanf("");
+  } else {
+    decode_unit<QT>(q, s, id * units_per_row + ur, v);
+  }
+  store_values<OUT>(out, t * T::kUnitWeights, v);
+}
+
+template <int QT, int OUT>
+static hipError_t dq(const uint8_t* q, const uint16_t* s, void* out,
+                     int64_t nblocks, hipStream_t stream) {
+  const int64_t nunits = nblocks * QTraits<QT>::kUnitsPerBlock;
+  const int64_t groups = (nunits + kDqThreads - 1) / kDqThreads;
+  hipLaunchKernelGGL((dequant_kernel<QT, OUT>), dim3((unsigned)groups),
+                     dim3(kDqThreads), 0, stream, q, s, out, nunits);
+  return hipGetLastError();
+}
+
+template <int QT, int OUT>
+static hipError_t dq_rows(const uint8_t* q, const uint16_t* s,
+                          const int64_t* ids, int64_t nids, int64_t nrows,
+                          int k, void* out, hipStream_t stream) {
+  const int upr = (k / 32) * QTraits<QT>::kUnitsPerBlock;
+  const int64_t total = nids * upr;
+  const int64_t groups = (total + kDqThreads - 1) / kDqThreads;
+  hipLaunchKernelGGL((dequant_rows_kernel<QT, OUT>), dim3((unsigned)groups),
+                     dim3(kDqThreads), 0, stream, q, s, ids, nids, nrows, upr,
+                     out);
+  return hipGetLastError();
+}
+
+template <int QT>
+static hipError_t dq_q(const uint8_t* q, const uint16_t* s, void* out,
+                       int64_t nblocks, int out_dtype, hipStream_t stream) {
+  switch (out_dtype) {
+    case 0: return dq<QT, 0>(q, s, out, nblocks, stream);
+    case 1: return dq<QT, 1>(q, s, out, nblocks, stream);
+    case 2: return dq<QT, 2>(q, s, out, nblocks, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int QT>
+static hipError_t dq_rows_q(const uint8_t* q, const uint16_t* s,
+                            const int64_t* ids, int64_t nids, int64_t nrows,
+                            int k, void* out, int out_dtype,
+                            hipStream_t stream) {
+  switch (out_dtype) {
+    case 0: return dq_rows<QT, 0>(q, s, ids, nids, nrows, k, out, stream);
+    case 1: return dq_rows<QT, 1>(q, s, ids, nids, nrows, k, out, stream);
+    case 2: return dq_rows<QT, 2>(q, s, ids, nids, nrows, k, out, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_dequant(const uint8_t* q, const uint16_t* s, void* out,
+                          int64_t nblocks, int qtype, int out_dtype,
+                          hipStream_t stream) {
+  switch (qtype) {
+    case 4: return dq_q<4>(q, s, out, nblocks, out_dtype, stream);
+    case 5: return dq_q<5>(q, s, out, nblocks, out_dtype, stream);
+    case 8: return dq_q<8>(q, s, out, nblocks, out_dtype, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_dequant_rows(const uint8_t* q, const uint16_t* s,
+                               const int64_t* ids, int64_t nids, int64_t nrows,
+                               int k, void* out, int qtype, int out_dtype,
+                               hipStream_t stream) {
+  switch (qtype) {
+    case 4: return dq_rows_q<4>(q, s, ids, nids, nrows, k, out, out_dtype, stream);
+    case 5: return dq_rows_q<5>(q, s, ids, nids, nrows, k, out, out_dtype, stream);
+    case 8: return dq_rows_q<8>(q, s, ids, nids, nrows, k, out, out_dtype, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace svq

@@ -1,0 +1,259 @@
+// Device-side building blocks shared by the GEMV and dequantize kernels:
+// per-quantization geometry and the in-register unpack of a lane's unit of
+// packed weights. gfx950 (CDNA4) only.
+//
+// A "unit" is the slice of one row's packed weights that one lane consumes per
+// step: one Q4_0 block (16 bytes, 32 weights), one Q5_0 block (20 bytes: the
+// uint32 high-bit mask then 16 nibble bytes, 32 weights) or half a Q8_0 block
+// (16 int8 bytes, 16 weights). Block layout and weight order follow the
+// reference decode (quantization.py:34-47): in a Q4_0/Q5_0 block, byte j's low
+// nibble is weight j and its high nibble weight j+16; Q5_0 weight j takes bit j
+// of the little-endian mask as its fifth bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace svq {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int QT> struct QTraits;
+
+// The GEMV turns every weight's unsigned code (nibble, 5-bit code or
+// int8 + 128) into the fp16 *subnormal* with the same bit pattern, i.e.
+// code * 2^-24, with one v_perm_b32 per pair of weights and no conversion
+// instruction. Products with fp16 activations are exact in fp32, so a block's
+// sum_j code_j * x_j is exact up to fp32 addition; the code offset is removed
+// by adding offset * sum_j x_j (kSxScale folds the 2^-24 scaling in), and the
+// result is rescaled once by kOutScale at the end.
+template <> struct QTraits<4> {
+  static constexpr int kBlockQ = 16;       // payload bytes per block
+  static constexpr int kUnitBytes = 16;    // payload bytes per unit
+  static constexpr int kUnitWeights = 32;  // weights per unit
+  static constexpr int kUnitsPerBlock = 1;
+  static constexpr int kWords = 4;         // dwords loaded per unit
+  static constexpr float kSxScale = -0x1p-21f;  // -8 * 2^-24
+  static constexpr float kOutScale = 0x1p24f;
+};
+template <> struct QTraits<5> {
+  static constexpr int kBlockQ = 20;
+  static constexpr int kUnitBytes = 20;
+  static constexpr int kUnitWeights = 32;
+  static constexpr int kUnitsPerBlock = 1;
+  static constexpr int kWords = 5;
+  // Codes are placed as 16 * code subnormals (see unpack_q5): -16 * 2^-20.
+  static constexpr float kSxScale = -0x1p-16f;
+  static constexpr float kOutScale = 0x1p20f;
+};
+template <> struct QTraits<8> {
+  static constexpr int kBlockQ = 32;
+  static constexpr int kUnitBytes = 16;
+  static constexpr int kUnitWeights = 16;
+  static constexpr int kUnitsPerBlock = 2;
+  static constexpr int kWords = 4;
+  static constexpr float kSxScale = -0x1p-17f;  // -128 * 2^-24
+  static constexpr float kOutScale = 0x1p24f;
+};
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a),
+                                __builtin_bit_cast(h2_t, b), c, false);
+}
+
+// v_perm_b32: byte i of the result is byte sel[i] of the 8-byte value
+// {hi, lo} (0-3 = lo, 4-7 = hi, 0x0c = zero byte).
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo,
+                                         uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+constexpr uint32_t kSelB01 = 0x0c010c00u;   // {lo.b0, 0, lo.b1, 0}
+constexpr uint32_t kSelB23 = 0x0c030c02u;   // {lo.b2, 0, lo.b3, 0}
+constexpr uint32_t kSelB01H = 0x05010400u;  // {lo.b0, hi.b0, lo.b1, hi.b1}
+constexpr uint32_t kSelB23H = 0x07030602u;  // {lo.b2, hi.b2, lo.b3, hi.b3}
+
+// Four mask bits (n < 16) spread to bit 0 of each byte:
+// n * 0x204081 = n + n<<7 + n<<14 + n<<21 puts bit i of n at bit 8i, with no
+// overlapping terms.
+__device__ __forceinline__ uint32_t spread4(uint32_t n) {
+  return (n * 0x00204081u) & 0x01010101u;
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Unpack one unit into fp16 pairs p[j] = (weight 2j, weight 2j+1) as
+// subnormal codes. Q4_0 returns the low-nibble half (weights 0-15, codes
+// 0..15) in p[0..7] and the high-nibble half (weights 16-31) in p[8..15] as
+// 16 * code, so the caller scales the second half's sum by 1/16. Q5_0 returns
+// all 32 as 16 * code (code = nibble | fifth bit << 4). Q8_0 returns the 16
+// weights of a half block as int8 + 128.
+template <int QT>
+__device__ __forceinline__ void unpack(const uint32_t (&w)[QTraits<QT>::kWords],
+                                       uint32_t (&p)[QTraits<QT>::kUnitWeights / 2]);
+
+template <>
+__device__ __forceinline__ void unpack<4>(const uint32_t (&w)[4],
+                                          uint32_t (&p)[16]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = w[i] & 0x0f0f0f0fu;  // codes of weights 4i..4i+3
+    const uint32_t hi = w[i] & 0xf0f0f0f0u;  // 16 * codes of 16+4i..16+4i+3
+    p[2 * i] = perm(0u, lo, kSelB01);
+    p[2 * i + 1] = perm(0u, lo, kSelB23);
+    p[8 + 2 * i] = perm(0u, hi, kSelB01);
+    p[8 + 2 * i + 1] = perm(0u, hi, kSelB23);
+  }
+}
+
+template <>
+__device__ __forceinline__ void unpack<5>(const uint32_t (&w)[5],
+                                          uint32_t (&p)[16]) {
+  const uint32_t qh = w[0];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t v = w[1 + i];
+    const uint32_t lo = (v << 4) & 0xf0f0f0f0u;  // 16 * low nibbles
+    const uint32_t hi = v & 0xf0f0f0f0u;         // 16 * high nibbles
+    const uint32_t blo = spread4((qh >> (4 * i)) & 15u);
+    const uint32_t bhi = spread4((qh >> (16 + 4 * i)) & 15u);
+    // Fifth bit as the high byte of each half: 16 * nibble + 256 * bit.
+    p[2 * i] = perm(blo, lo, kSelB01H);
+    p[2 * i + 1] = perm(blo, lo, kSelB23H);
+    p[8 + 2 * i] = perm(bhi, hi, kSelB01H);
+    p[8 + 2 * i + 1] = perm(bhi, hi, kSelB23H);
+  }
+}
+
+template <>
+__device__ __forceinline__ void unpack<8>(const uint32_t (&w)[4],
+                                          uint32_t (&p)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t v = w[i] ^ 0x80808080u;  // int8 -> int8 + 128
+    p[2 * i] = perm(0u, v, kSelB01);
+    p[2 * i + 1] = perm(0u, v, kSelB23);
+  }
+}
+
+// Dot product of one unpacked unit with its activations xv (fp16 pairs in
+// natural order), started from `start` (the offset term). Result is in units
+// of the code scaling (2^-24, or 2^-20 for Q5_0).
+template <int QT>
+__device__ __forceinline__ float unit_dot(const uint32_t (&p)[QTraits<QT>::kUnitWeights / 2],
+                                          const uint32_t (&xv)[QTraits<QT>::kUnitWeights / 2],
+                                          float start);
+
+template <>
+__device__ __forceinline__ float unit_dot<4>(const uint32_t (&p)[16],
+                                             const uint32_t (&xv)[16],
+                                             float start) {
+  float lo = start, hi = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) lo = dot2(p[j], xv[j], lo);
+#pragma unroll
+  for (int j = 8; j < 16; ++j) hi = dot2(p[j], xv[j], hi);
+  return __builtin_fmaf(hi, 0.0625f, lo);
+}
+
+template <>
+__device__ __forceinline__ float unit_dot<5>(const uint32_t (&p)[16],
+                                             const uint32_t (&xv)[16],
+                                             float start) {
+  // Two chains for latency; both halves share the 16 * code scaling.
+  float a = start, b = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a = dot2(p[j], xv[j], a);
+#pragma unroll
+  for (int j = 8; j < 16; ++j) b = dot2(p[j], xv[j], b);
+  return a + b;
+}
+
+template <>
+__device__ __forceinline__ float unit_dot<8>(const uint32_t (&p)[8],
+                                             const uint32_t (&xv)[8],
+                                             float start) {
+  float a = start, b = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) a = dot2(p[j], xv[j], a);
+#pragma unroll
+  for (int j = 4; j < 8; ++j) b = dot2(p[j], xv[j], b);
+  return a + b;
+}
+
+// Signed integer weights of one unit (for dequantization), exactly as the
+// reference computes them (quantization.py:34-47).
+template <int QT>
+__device__ __forceinline__ void unit_codes(const uint32_t (&w)[QTraits<QT>::kWords],
+                                           int (&v)[QTraits<QT>::kUnitWeights]);
+
+template <>
+__device__ __forceinline__ void unit_codes<4>(const uint32_t (&w)[4], int (&v)[32]) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t byte = (w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+    v[j] = (int)(byte & 15u) - 8;
+    v[j + 16] = (int)(byte >> 4) - 8;
+  }
+}
+
+template <>
+__device__ __forceinline__ void unit_codes<5>(const uint32_t (&w)[5], int (&v)[32]) {
+  const uint32_t qh = w[0];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t byte = (w[1 + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
+    v[j] = (int)((byte & 15u) | (((qh >> j) & 1u) << 4)) - 16;
+    v[j + 16] = (int)((byte >> 4) | (((qh >> (j + 16)) & 1u) << 4)) - 16;
+  }
+}
+
+template <>
+__device__ __forceinline__ void unit_codes<8>(const uint32_t (&w)[4], int (&v)[16]) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    v[j] = (int)(int8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xffu);
+}
+
+// Buffer resource over `bytes` bytes from the wave-uniform `base`: loads use
+// 32-bit offsets (no per-lane 64-bit address arithmetic) and reads beyond
+// `bytes` return zeros instead of touching memory. The last word is the gfx9
+// family's raw-buffer format (32-bit data format, no swizzle).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
+                                                           uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)bytes, 0x00020000);
+}
+
+// Load one unit's dwords at byte offset `off` of a buffer resource.
+template <int QT>
+__device__ __forceinline__ void load_unit_buf(__amdgpu_buffer_rsrc_t r,
+                                              uint32_t off,
+                                              uint32_t (&w)[QTraits<QT>::kWords]) {
+  const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  if constexpr (QT == 5) w[4] = __builtin_amdgcn_raw_buffer_load_b32(r, off + 16, 0, 0);
+}
+
+// Load one unit's dwords. Q4_0/Q8_0 units are 16-byte aligned (one
+// global_load_dwordx4); Q5_0 units are 20 bytes apart, i.e. dword aligned:
+// one dwordx4 plus one dword.
+template <int QT>
+__device__ __forceinline__ void load_unit(const uint8_t* p,
+                                          uint32_t (&w)[QTraits<QT>::kWords]) {
+  if constexpr (QT == 5) {
+    typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+    const u32x4a4 a = *reinterpret_cast<const u32x4a4*>(p);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = *reinterpret_cast<const uint32_t*>(p + 16);
+  } else {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(p);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  }
+}
+
+}  // namespace svq

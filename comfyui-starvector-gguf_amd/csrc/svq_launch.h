@@ -1,0 +1,43 @@
+// Host-side launch interface between the C ABI (svq_api.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace svq {
+
+struct GemvArgs {
+  const uint16_t* x;     // fp16 [m, k]
+  const uint8_t* q;      // SoA payload
+  const uint16_t* s;     // fp16 scale bits
+  const uint16_t* bias;  // fp16 [n] or nullptr
+  void* y;               // [m, n] fp16 or fp32
+  int n, k;
+  int lg_g;         // log2 of the lanes that share a row
+  int chunk_units;  // units of x staged in LDS at a time
+  int y_f32;
+};
+
+struct GemvShape {
+  int m;
+  int rows_per_group;  // R: rows owned by one lane group
+  int groups;          // workgroups in the grid
+  int chunk_units;
+  int lg_g;
+};
+
+// Kernel launchers (svq_gemv.hip, svq_dequant.hip).
+hipError_t launch_gemv(const GemvArgs& a, const GemvShape& sh, int qtype,
+                       hipStream_t stream);
+int lds_bytes_per_unit(int qtype);
+int units_per_block(int qtype);
+
+hipError_t launch_dequant(const uint8_t* q, const uint16_t* s, void* out,
+                          int64_t nblocks, int qtype, int out_dtype,
+                          hipStream_t stream);
+hipError_t launch_dequant_rows(const uint8_t* q, const uint16_t* s,
+                               const int64_t* ids, int64_t nids, int64_t nrows,
+                               int k, void* out, int qtype, int out_dtype,
+                               hipStream_t stream);
+
+}  // namespace svq

@@ -1,0 +1,104 @@
+/*
+ * svq.h - C ABI of the gfx950 GGUF SoA dequantize + GEMV library (libsvq.so).
+ *
+ * Weights use the structure-of-arrays layout that the reference builds at load
+ * time (quantization.py:67-90, `pack_gguf_soa`): for an N x K matrix with
+ * K % 32 == 0 there are N * K / 32 blocks of 32 weights, block b = row * (K/32)
+ * + kb, and
+ *   q[b * W .. b * W + W)  the block payload without its scale, W = 16 (Q4_0),
+ *                          20 (Q5_0: uint32 LE high-bit mask, then 16 nibble
+ *                          bytes) or 32 (Q8_0: int8);
+ *   s[b]                   the fp16 bits of the block scale d.
+ * Weight j of a block (App. of the reference layout, quantization.py:34-47):
+ *   Q8_0: d * (int8)q[j]
+ *   Q4_0: d * ((q[j % 16] >> 4 * (j / 16)) & 15) - 8)
+ *   Q5_0: d * ((nibble(j) | ((qh >> j) & 1) << 4) - 16)
+ *
+ * Every pointer is a device pointer owned by the caller; the library never
+ * allocates, frees or retains memory, never synchronizes and only enqueues
+ * kernels on `stream` (a hipStream_t, NULL = the null stream), so every entry
+ * point may be captured into a HIP graph.
+ *
+ * Return codes: 0 on success; a negative SVQ_E* code when an argument is
+ * rejected (checked before any HIP call, so it needs no GPU); a positive
+ * hipError_t when a HIP call fails. svq_last_error() describes the last
+ * failure of the calling thread.
+ */
+#ifndef SVQ_H
+#define SVQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SVQ_ABI_VERSION 1
+
+/* Quantization codes: the reference's kernel codes (quantization.py:120). */
+#define SVQ_Q4_0 4
+#define SVQ_Q5_0 5
+#define SVQ_Q8_0 8
+
+/* Element types of dequantized or GEMV outputs. */
+#define SVQ_F32 0
+#define SVQ_F16 1
+#define SVQ_BF16 2
+
+#define SVQ_MAX_ROWS 8 /* largest M of svq_gemv */
+
+#define SVQ_E_QTYPE (-1)   /* qtype is not 4, 5 or 8 */
+#define SVQ_E_SHAPE (-2)   /* bad m, n, k (k % 32, sizes, ranges) */
+#define SVQ_E_NULL (-3)    /* a required pointer is NULL */
+#define SVQ_E_DTYPE (-4)   /* unsupported output element type */
+#define SVQ_E_RANGE (-5)   /* a size exceeds the 32-bit offsets the kernels use */
+#define SVQ_E_ALIGN (-6)   /* x / q / out not aligned for 16-byte accesses
+                              (q: 4 bytes for Q5_0; s, bias: 2 bytes) */
+
+/* Version of this ABI (SVQ_ABI_VERSION). */
+int svq_abi_version(void);
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char *svq_last_error(void);
+
+/*
+ * y[m, n] = sum_k x[m, k] * W[n, k] + bias[n] for 1 <= m <= SVQ_MAX_ROWS.
+ * Replaces `soa_gemv` (quantization.py:232-265) and the `_soa_gemv` Triton
+ * kernel (quantization.py:171-229) it launches, and also covers the beam
+ * widths 3..8 that the reference sends to `_soa_mm` (quantization.py:313-319).
+ *   x     fp16 [m, k] row-major
+ *   q, s  SoA payload and fp16 scale bits of the n x k matrix
+ *   bias  fp16 [n] or NULL
+ *   y     [m, n] row-major, fp16 (y_dtype SVQ_F16, as the reference stores)
+ *         or fp32 (SVQ_F32)
+ * Each block's integer dot product is accumulated in fp32 and multiplied by
+ * its scale once (quantization.py:199, 215); bias is added in fp32 before the
+ * final rounding.
+ */
+int svq_gemv(const void *x, const uint8_t *q, const uint16_t *s,
+             const uint16_t *bias, void *y, int m, int n, int k, int qtype,
+             int y_dtype, void *stream);
+
+/*
+ * out[b * 32 + j] = weight j of block b, for b < nblocks, rounded from the
+ * exact fp32 product to out_dtype (SVQ_F32 / SVQ_F16 / SVQ_BF16, round to
+ * nearest even). Replaces `dequantize_soa` (quantization.py:93-105) on the GPU.
+ */
+int svq_dequant(const uint8_t *q, const uint16_t *s, void *out,
+                int64_t nblocks, int qtype, int out_dtype, void *stream);
+
+/*
+ * Row gather + dequantize: out[i, :] = row ids[i] of the nrows x k matrix,
+ * for i < nids (ids int64). Replaces the `index_select` + `dequantize_soa`
+ * pair of `GGUFEmbedding.forward` (quantization.py:421-446). An id outside
+ * [0, nrows) yields a row of NaN instead of a memory access.
+ */
+int svq_dequant_rows(const uint8_t *q, const uint16_t *s, const int64_t *ids,
+                     int64_t nids, int64_t nrows, int k, void *out,
+                     int qtype, int out_dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SVQ_H */

@@ -1,0 +1,97 @@
+"""The C ABI without a GPU: libsvq.so loads, exports every function that
+include/svq.h declares, and rejects bad arguments before any HIP call."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import starvector_amd._native as native
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "svq.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(svq_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    assert {"svq_abi_version", "svq_last_error", "svq_gemv", "svq_dequant",
+            "svq_dequant_rows"} <= set(names)
+
+
+def test_library_exports_every_declared_function():
+    lib = native.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
+
+
+def test_abi_version():
+    assert native.load().svq_abi_version() == native.ABI_VERSION == 1
+
+
+FAKE = 1 << 20  # a 16-byte aligned non-null address; never dereferenced
+
+
+def gemv(**kw):
+    args = dict(x=FAKE, q=FAKE, s=FAKE, bias=None, y=FAKE, m=1, n=8, k=64, qtype=4,
+                y_dtype=1, stream=None)
+    args.update(kw)
+    lib = native.load()
+    return lib.svq_gemv(args["x"], args["q"], args["s"], args["bias"], args["y"], args["m"],
+                        args["n"], args["k"], args["qtype"], args["y_dtype"], args["stream"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(qtype=2), -1), (dict(qtype=6), -1),
+    (dict(m=0), -2), (dict(m=9), -2), (dict(n=0), -2), (dict(k=0), -2), (dict(k=48), -2),
+    (dict(k=1 << 25), -5), (dict(n=(1 << 30) + 1), -5),
+    (dict(x=None), -3), (dict(q=None), -3), (dict(s=None), -3), (dict(y=None), -3),
+    (dict(y_dtype=2), -4), (dict(y_dtype=7), -4),
+    (dict(x=FAKE + 8), -6), (dict(q=FAKE + 4), -6), (dict(q=FAKE + 4, qtype=5), None),
+    (dict(s=FAKE + 1), -6), (dict(bias=FAKE + 1), -6), (dict(y=FAKE + 1), -6),
+])
+def test_gemv_rejects_bad_arguments(kw, code):
+    if code is None:
+        # Q5_0 only needs 4-byte payload alignment: pair it with a rejected
+        # shape so the call still returns before any launch.
+        kw = dict(kw, k=48)
+        code = -2
+    assert gemv(**kw) == code
+    assert native.load().svq_last_error().decode()
+
+
+def test_dequant_rejects_bad_arguments():
+    lib = native.load()
+    assert lib.svq_dequant(FAKE, FAKE, FAKE, 4, 3, 0, None) == -1
+    assert lib.svq_dequant(FAKE, FAKE, FAKE, -1, 4, 0, None) == -2
+    assert lib.svq_dequant(FAKE, FAKE, FAKE, 4, 4, 3, None) == -4
+    assert lib.svq_dequant(None, FAKE, FAKE, 4, 4, 0, None) == -3
+    assert lib.svq_dequant(FAKE, FAKE, FAKE + 4, 4, 4, 0, None) == -6
+    assert lib.svq_dequant(FAKE, FAKE, FAKE, 0, 4, 0, None) == 0  # empty: no launch
+
+
+def test_dequant_rows_rejects_bad_arguments():
+    lib = native.load()
+    call = lambda **kw: lib.svq_dequant_rows(
+        kw.get("q", FAKE), kw.get("s", FAKE), kw.get("ids", FAKE), kw.get("nids", 2),
+        kw.get("nrows", 5), kw.get("k", 64), kw.get("out", FAKE), kw.get("qtype", 8),
+        kw.get("dt", 1), None)
+    assert call(qtype=1) == -1
+    assert call(k=40) == -2
+    assert call(nrows=0) == -2
+    assert call(dt=5) == -4
+    assert call(ids=None) == -3
+    assert call(ids=FAKE + 4) == -6
+    assert call(nids=0) == 0
+
+
+def test_error_message_names_the_problem():
+    gemv(m=11)
+    assert "m=11" in native.load().svq_last_error().decode()
