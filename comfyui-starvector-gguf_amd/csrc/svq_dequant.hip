@@ -33,9 +33,17 @@ __device__ __forceinline__ void store_values(void* out, int64_t first,
   } else {
     uint16_t h[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
-      h[i] = OUT == 1 ? __builtin_bit_cast(uint16_t, (_Float16)v[i])
-                      : f32_to_bf16_rne(v[i]);
+    for (int i = 0; i < NV; ++i) {
+      if constexpr (OUT == 1) {
+        // The backend fuses product + conversion into v_fma_mixlo_f16 with a
+        // +0 addend, which turns a -0 product into +0; the fp16 result always
+        // carries the fp32 value's sign, so restore it from the fp32 bits.
+        const uint32_t sign = (__builtin_bit_cast(uint32_t, v[i]) >> 16) & 0x8000u;
+        h[i] = __builtin_bit_cast(uint16_t, (_Float16)v[i]) | (uint16_t)sign;
+      } else {
+        h[i] = f32_to_bf16_rne(v[i]);
+      }
+    }
     u32x4* o = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(out) + first);
 #pragma unroll
     for (int i = 0; i < NV / 8; ++i)

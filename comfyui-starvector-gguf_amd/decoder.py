@@ -1,0 +1,309 @@
+"""StarCoder2-style decoder harness that drives the quantized GEMV.
+
+Restates the decode path of the reference's runtime_8b.py (Starcoder2Block
+:20-57, Starcoder2 :60-110), the KV-cache / graph machinery of
+runtime_shared.py (CachedDecoding :345-394) and its beam sampling
+(_penalize/_warp/_beam_sample :170-265). Every quantized linear is a
+`GGUFLinear` over SoA arrays, so each decode step runs the HIP GEMV 4 x layers
++ 1 times (q, k and v are one fused linear: their SoA rows concatenated, a pure
+byte concatenation). Attention, LayerNorm, RoPE, sampling and the KV cache
+stay in PyTorch.
+
+Attention products are arranged so that no batched product takes a transposed
+view as its right operand: decode computes K @ q^T with a contiguous q^T, and
+prefill multiplies by a contiguous K^T.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .quantization import BLOCK_BYTES, GGUFEmbedding, GGUFLinear, tied_head
+
+# Sampling settings of the reference (runtime_shared.py:148-150).
+TOP_K = 50
+REPETITION_PENALTY = 3.1
+LENGTH_PENALTY = -1.0
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    """StarCoder2-8B-style decoder shape (the reference's runtime_8b.py reads
+    these from the GGUF's embedded config; rope_theta and sliding_window
+    default as in runtime_8b.py:71-72)."""
+    hidden: int = 4608
+    heads: int = 36
+    kv_heads: int = 4
+    inner: int = 18432
+    layers: int = 32
+    vocab: int = 49152
+    rope_theta: float = 1e6
+    window: int = 4096
+    context: int = 16000
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads
+
+
+def random_soa(qtype: str, n: int, k: int, generator: torch.Generator, device) -> tuple:
+    """Seeded synthetic SoA arrays: uniform payload bytes (uniform codes;
+    Q8_0 int8 in [-127, 127]) and fp16 scales uniform in [1e-3, 2e-2]."""
+    blocks = n * k // 32
+    if qtype == "Q8_0":
+        q = torch.randint(-127, 128, (blocks * 32,), generator=generator, device=device,
+                          dtype=torch.int8).view(torch.uint8)
+    else:
+        q = torch.randint(0, 256, (blocks * (BLOCK_BYTES[qtype] - 2),), generator=generator,
+                          device=device, dtype=torch.uint8)
+    d = torch.rand(blocks, generator=generator, device=device) * (2e-2 - 1e-3) + 1e-3
+    return q, d.half().view(torch.uint8)
+
+
+def random_linear(qtype, n, k, generator, device, bias=True):
+    layer = GGUFLinear(k, n)
+    layer.set_soa(qtype, (n, k), *random_soa(qtype, n, k, generator, device))
+    if bias:
+        layer.set_dense("bias", (torch.randn(n, generator=generator, device=device) * 0.02).half())
+    return layer
+
+
+def random_norm(width, generator, device):
+    norm = nn.LayerNorm(width, eps=1e-5, device=device, dtype=torch.float16)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.05 * torch.randn(width, generator=generator, device=device))
+        norm.bias.copy_(0.02 * torch.randn(width, generator=generator, device=device))
+    norm.weight.requires_grad_(False)
+    norm.bias.requires_grad_(False)
+    return norm
+
+
+def rotate(x, cos, sin):
+    """Rotary embedding over rotated halves (runtime_8b.py:14-17)."""
+    first, second = x.chunk(2, dim=-1)
+    return x * cos + torch.cat((-second, first), dim=-1) * sin
+
+
+class Starcoder2Block(nn.Module):
+    """Grouped-query block writing its keys/values into a fixed cache
+    (runtime_8b.py:20-57), with q/k/v as one fused quantized linear."""
+
+    def __init__(self, cfg: DecoderConfig, qtype, generator, device):
+        super().__init__()
+        self.cfg = cfg
+        hd = cfg.head_dim
+        self.input_layernorm = random_norm(cfg.hidden, generator, device)
+        self.qkv_proj = random_linear(qtype, cfg.hidden + 2 * cfg.kv_heads * hd, cfg.hidden,
+                                      generator, device)
+        self.o_proj = random_linear(qtype, cfg.hidden, cfg.hidden, generator, device)
+        self.post_attention_layernorm = random_norm(cfg.hidden, generator, device)
+        self.c_fc = random_linear(qtype, cfg.inner, cfg.hidden, generator, device)
+        self.c_proj = random_linear(qtype, cfg.hidden, cfg.inner, generator, device)
+
+    def forward(self, x, cos, sin, keys, values, position=None, bias=None):
+        cfg = self.cfg
+        hd, heads, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
+        rows, length, hidden = x.shape
+        qkv = self.qkv_proj(self.input_layernorm(x))
+        q, k, v = qkv.split((hidden, kvh * hd, kvh * hd), -1)
+        q = rotate(q.view(rows, length, heads, hd).transpose(1, 2), cos, sin)
+        k = rotate(k.view(rows, length, kvh, hd).transpose(1, 2), cos, sin)
+        v = v.view(rows, length, kvh, hd).transpose(1, 2)
+        group = heads // kvh
+        if position is None:
+            keys[:, :, :length] = k
+            values[:, :, :length] = v
+            out = causal_attention(q, k, v, group).reshape(rows, length, hidden)
+        else:
+            keys.index_copy_(2, position, k)
+            values.index_copy_(2, position, v)
+            span = keys.shape[2]
+            # scores^T = K @ q^T per (row, kv head): [span, hd] @ [hd, group].
+            kb = keys.flatten(0, 1)
+            qt = q.reshape(rows * kvh, group, hd).transpose(1, 2).contiguous()
+            scores = torch.bmm(kb, qt).transpose(1, 2) * hd ** -0.5 + bias
+            probs = torch.softmax(scores, -1, dtype=torch.float32).to(x.dtype).contiguous()
+            out = torch.bmm(probs, values.flatten(0, 1)).view(rows, 1, hidden)
+            del span
+        x = x + self.o_proj(out)
+        return x + self.c_proj(F.gelu(self.c_fc(self.post_attention_layernorm(x)), approximate="tanh"))
+
+
+def causal_attention(q, k, v, group):
+    """Causal GQA attention for prefill: q [B, H, T, D], k/v [B, Hkv, T, D];
+    returns [B, T, H, D]. fp32 softmax; the key operand is transposed into a
+    contiguous tensor before the product."""
+    b, h, t, d = q.shape
+    k = k.repeat_interleave(group, dim=1)
+    v = v.repeat_interleave(group, dim=1).contiguous()
+    kt = k.transpose(-1, -2).contiguous()
+    out = torch.empty((b, h, t, d), dtype=q.dtype, device=q.device)
+    mask = torch.full((t, t), float("-inf"), device=q.device).triu_(1)
+    chunk = 4  # heads per product, bounds the fp32 score tensor
+    for h0 in range(0, h, chunk):
+        s = torch.matmul(q[:, h0:h0 + chunk].contiguous(), kt[:, h0:h0 + chunk]).float()
+        p = torch.softmax(s * d ** -0.5 + mask, -1).to(q.dtype)
+        out[:, h0:h0 + chunk] = torch.matmul(p, v[:, h0:h0 + chunk])
+    return out.transpose(1, 2)
+
+
+class Starcoder2Decoder(nn.Module):
+    """StarCoder2-style decoder with a tied quantized embedding / head
+    (runtime_8b.py:60-110), built from seeded synthetic SoA weights."""
+
+    def __init__(self, cfg: DecoderConfig, qtype="Q4_0", head_qtype=None, seed=0, device="cuda"):
+        super().__init__()
+        self.cfg = cfg
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.embed_tokens = GGUFEmbedding(cfg.vocab, cfg.hidden)
+        hq = head_qtype or qtype
+        self.embed_tokens.set_soa(hq, (cfg.vocab, cfg.hidden), *random_soa(hq, cfg.vocab, cfg.hidden, g, device))
+        self.embed_tokens.output_dtype = torch.float16
+        self.layers = nn.ModuleList([Starcoder2Block(cfg, qtype, g, device) for _ in range(cfg.layers)])
+        self.norm = random_norm(cfg.hidden, g, device)
+        self.lm_head = tied_head(self.embed_tokens)
+        self.context = cfg.context
+
+    def _rope(self, positions, dtype):
+        hd = self.cfg.head_dim
+        inv_freq = 1.0 / (self.cfg.rope_theta ** (
+            torch.arange(0, hd, 2, device=positions.device, dtype=torch.float32) / hd))
+        angles = positions.float()[:, None] * inv_freq
+        angles = torch.cat((angles, angles), -1)
+        return angles.cos().to(dtype), angles.sin().to(dtype)
+
+    def embed(self, ids):
+        return self.embed_tokens(ids)
+
+    def prefill(self, embeddings, rows, capacity):
+        """Encode the prompt once (batch 1); its cache serves all `rows`."""
+        cfg = self.cfg
+        length = embeddings.shape[1]
+        shape = (cfg.layers, rows, cfg.kv_heads, capacity, cfg.head_dim)
+        keys = torch.zeros(shape, device=embeddings.device, dtype=embeddings.dtype)
+        values = torch.zeros_like(keys)
+        cos, sin = self._rope(torch.arange(length, device=embeddings.device), embeddings.dtype)
+        x = embeddings
+        for layer, lk, lv in zip(self.layers, keys, values):
+            x = layer(x, cos, sin, lk, lv)
+        logits = self.lm_head(self.norm(x[:, -1]))
+        return CachedDecoding(self, keys, values, length), logits.expand(rows, -1)
+
+    def decode(self, tokens, position, keys, values, span):
+        """One token per row at `position`, attending the first `span` slots."""
+        slots = torch.arange(span, device=keys.device)
+        hidden_slots = (slots > position) | (slots <= position - self.cfg.window)
+        bias = torch.zeros(span, device=keys.device, dtype=keys.dtype).masked_fill_(hidden_slots, float("-inf"))
+        cos, sin = self._rope(position, keys.dtype)
+        x = self.embed_tokens(tokens)[:, None]
+        for layer, lk, lv in zip(self.layers, keys, values):
+            x = layer(x, cos, sin, lk[:, :, :span], lv[:, :, :span], position, bias)
+        return self.lm_head(self.norm(x[:, 0]))
+
+
+class CachedDecoding:
+    """KV cache and graph-captured decode steps of one generation call
+    (runtime_shared.py:345-394): one HIP graph per power-of-two span of at
+    least 512 slots, captured after an eager warm-up on a side stream."""
+
+    def __init__(self, model, keys, values, length):
+        self.model, self.keys, self.values, self.length = model, keys, values, length
+        self.tokens = torch.zeros(keys.shape[1], dtype=torch.long, device=keys.device)
+        self.position = torch.full((1,), length, dtype=torch.long, device=keys.device)
+        self.graphs = {}
+
+    def span(self):
+        return min(self.keys.shape[-2], max(512, 1 << self.length.bit_length()))
+
+    def _decode(self, span):
+        return self.model.decode(self.tokens, self.position, self.keys, self.values, span)
+
+    def step(self, tokens):
+        span = self.span()
+        self.tokens.copy_(tokens)
+        if self.keys.device.type != "cuda":
+            logits = self._decode(span)
+        else:
+            if span not in self.graphs:
+                stream = torch.cuda.Stream()
+                stream.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(stream):
+                    self._decode(span)  # warm-up; rewrites only this step's cache slot
+                torch.cuda.current_stream().wait_stream(stream)
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, capture_error_mode="thread_local"):
+                    output = self._decode(span)
+                self.graphs[span] = graph, output
+            graph, logits = self.graphs[span]
+            graph.replay()
+        self.position += 1
+        self.length += 1
+        return logits
+
+    def reorder(self, parents):
+        """Copy each row's parent beam cache into rows that changed parent."""
+        rows = [row for row, parent in enumerate(parents) if parent != row]
+        if rows:
+            sources = [parents[row] for row in rows]
+            self.keys[:, rows, ..., :self.length, :] = self.keys[:, sources, ..., :self.length, :]
+            self.values[:, rows, ..., :self.length, :] = self.values[:, sources, ..., :self.length, :]
+
+
+def penalize(scores, seen):
+    """Repetition penalty over generated tokens (runtime_shared.py:170-173)."""
+    penalized = torch.where(scores < 0, scores * REPETITION_PENALTY, scores / REPETITION_PENALTY)
+    return torch.where(seen, penalized, scores)
+
+
+def warp(scores, temperature, top_p, keep):
+    """Temperature, top-k and top-p warpers, in that order (runtime_shared.py:176-187)."""
+    if temperature != 1.0:
+        scores = scores / temperature
+    threshold = torch.topk(scores, max(TOP_K, keep))[0][..., -1:]
+    scores = scores.masked_fill(scores < threshold, float("-inf"))
+    if top_p < 1.0:
+        ordered, order = torch.sort(scores, descending=False)
+        remove = ordered.softmax(-1).cumsum(-1) <= 1 - top_p
+        remove[..., -keep:] = False
+        scores = scores.masked_fill(remove.scatter(-1, order, remove), float("-inf"))
+    return scores
+
+
+def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, capacity=None,
+               on_prefill=None):
+    """Beam sampling (runtime_shared.py:214-265) for a fixed number of decode
+    steps: every step samples 2 * beams continuations from all beams, keeps
+    the best `beams`, reorders the cache and decodes. End-of-sequence tokens
+    do not stop it, so every call performs exactly `steps` decode steps.
+    Returns (best token sequence, per-step running scores)."""
+    keep = 2 * beams
+    capacity = capacity or embeddings.shape[1] + steps + 1
+    decoding, logits = decoder.prefill(embeddings, beams, capacity)
+    if on_prefill is not None:
+        on_prefill()
+    device, vocab = logits.device, logits.shape[-1]
+    running = [[] for _ in range(beams)]
+    running_scores = [0.0] + [-1e9] * (beams - 1)
+    seen = torch.zeros((beams, vocab), dtype=torch.bool, device=device)
+    for step in range(steps):
+        log_probs = warp(penalize(torch.log_softmax(logits.float(), -1), seen), temperature, top_p, 2)
+        scores = (log_probs + torch.tensor(running_scores, device=device)[:, None]).view(1, -1)
+        probs = scores.softmax(-1)
+        picks = torch.multinomial(probs, min(keep, int(torch.count_nonzero(probs))))
+        picked = scores.gather(1, picks)[0].tolist()
+        parents, tokens = zip(*(divmod(pick, vocab) for pick in picks[0].tolist()))
+        order = sorted(range(len(picked)), key=picked.__getitem__, reverse=True)[:beams]
+        running_scores = [picked[j] for j in order] + [-1e9] * (beams - len(order))
+        order += [order[0]] * (beams - len(order))
+        running = [running[parents[j]] + [tokens[j]] for j in order]
+        selected = torch.tensor([parents[j] for j in order], device=device)
+        next_tokens = torch.tensor([tokens[j] for j in order], device=device)
+        seen = seen[selected]
+        seen[torch.arange(beams, device=device), next_tokens] = True
+        decoding.reorder([parents[j] for j in order])
+        logits = decoding.step(next_tokens)
+    return running[0], running_scores

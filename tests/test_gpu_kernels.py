@@ -49,6 +49,17 @@ def hip_gemv(x, q, s, qtype, n, bias=None, out_dtype=torch.float16):
     return y
 
 
+def assert_bits(got: np.ndarray, want: np.ndarray, label: str) -> None:
+    """Bit equality; on failure report the first mismatches compactly."""
+    got = np.ascontiguousarray(got).reshape(-1)
+    want = np.ascontiguousarray(want).reshape(-1)
+    assert got.shape == want.shape, (label, got.shape, want.shape)
+    bad = np.nonzero(got != want)[0]
+    if bad.size:
+        head = ", ".join(f"[{i}] got {int(got[i]):#x} want {int(want[i]):#x}" for i in bad[:8])
+        raise AssertionError(f"{label}: {bad.size} of {got.size} differ: {head}")
+
+
 def bf16_rne_bits(f32: np.ndarray) -> np.ndarray:
     b = f32.astype(np.float32).view(np.uint32).astype(np.uint64)
     r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
@@ -72,14 +83,16 @@ def test_dequant_golden_bit_exact(cuda_device, qtype):
         want = fx["dequant_bits"].reshape(-1)
         out32 = torch.empty(n * k, dtype=torch.float32, device=cuda_device)
         native.dequant(q, s, out32, qtype)
-        assert np.array_equal(out32.cpu().numpy().view(np.int32), want), name
+        assert_bits(out32.cpu().numpy().view(np.uint32), want.view(np.uint32), f"{name} fp32")
         f32 = want.view(np.float32)
         out16 = torch.empty(n * k, dtype=torch.float16, device=cuda_device)
         native.dequant(q, s, out16, qtype)
-        assert np.array_equal(out16.cpu().numpy().view(np.uint16), f32.astype(np.float16).view(np.uint16)), name
+        with np.errstate(over="ignore"):
+            want16 = f32.astype(np.float16).view(np.uint16)
+        assert_bits(out16.cpu().numpy().view(np.uint16), want16, f"{name} fp16")
         outb = torch.empty(n * k, dtype=torch.bfloat16, device=cuda_device)
         native.dequant(q, s, outb, qtype)
-        assert np.array_equal(outb.view(torch.int16).cpu().numpy().view(np.uint16), bf16_rne_bits(f32)), name
+        assert_bits(outb.view(torch.int16).cpu().numpy().view(np.uint16), bf16_rne_bits(f32), f"{name} bf16")
 
 
 @pytest.mark.parametrize("qtype", QTYPES)
@@ -90,7 +103,7 @@ def test_dequant_seeded_matrix_bit_exact(cuda_device, qtype):
     want = orc.dequantize_soa(q, s, qtype, (n, k)).reshape(-1)
     out = torch.empty(n * k, dtype=torch.float32, device=cuda_device)
     native.dequant(to_dev(q, cuda_device), to_dev(s, cuda_device), out, qtype)
-    assert np.array_equal(out.cpu().numpy().view(np.int32), want.view(np.int32))
+    assert_bits(out.cpu().numpy().view(np.uint32), want.view(np.uint32), f"{qtype} seeded")
 
 
 @pytest.mark.parametrize("qtype", QTYPES)
