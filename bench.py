@@ -165,6 +165,106 @@ def sweep_cases():
     return cases
 
 
+def profile_pass(dev, stream):
+    """Eager launches, one dispatch per GEMV, for kernel traces and counters."""
+    pool = Pool(dev, q_bytes=3 * 2**30, s_bytes=2**29)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    xs = {k: torch.randn((STEP_M, k), device=dev, generator=gen).half() for k in (4608, 18432)}
+    calls = {}
+    for name, n, k, bias in STEP_SHAPES:
+        cps = pool.copies(STEP_QTYPE, n, k, COPIES)
+        b = torch.randn(n, device=dev, generator=gen).half() if bias else None
+        y = torch.empty((STEP_M, n), dtype=torch.float16, device=dev)
+        calls[name] = [make_call(xs[k], q, s, y, STEP_QTYPE, b) for q, s in cps]
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            for i in range(COPIES):
+                for name, *_ in STEP_SHAPES:
+                    calls[name][i]()
+        stream.synchronize()
+        src = torch.empty(2**28, dtype=torch.uint8, device=dev)
+        dst = [torch.empty_like(src) for _ in range(4)]
+        for i in range(16):
+            dst[i % 4].copy_(src)
+        stream.synchronize()
+    log(f"profile pass done: {2 * COPIES * len(STEP_SHAPES)} GEMV dispatches, 16 copies of {2**28} bytes")
+
+
+def _is_gemv(name):
+    return name.startswith("void svq::") and "gemv" in name
+
+
+def _short_kernel(name):
+    for junk in ("void svq::", "(anonymous namespace)::", "(svq::GemvArgs)"):
+        name = name.replace(junk, "")
+    return name
+
+
+def _read_csv(path):
+    import csv
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def summarize(root: Path):
+    """Per-shape averages from rocprofv3 CSVs of `bench.py --profile` runs.
+
+    GEMV dispatches are mapped to shapes by their order (the profile pass
+    launches the step shapes round-robin); the torch copy of 256 MiB is the
+    known-size kernel whose FETCH_SIZE / WRITE_SIZE give the counters' scale.
+    """
+    shapes = [(name, n, k, bias) for name, n, k, bias in STEP_SHAPES]
+    out = []
+    traces = sorted(root.rglob("*kernel_trace.csv"))
+    if traces:
+        rows = _read_csv(traces[0])
+        gemv = [r for r in rows if _is_gemv(r["Kernel_Name"])]
+        copies = [r for r in rows if "copyBuffer" in r["Kernel_Name"]]
+        out.append(f"kernel trace: {traces[0].relative_to(root)} ({len(gemv)} GEMV dispatches)")
+        out.append("| shape | kernel | grid | VGPR | LDS B | dispatches | avg us | min us | GB/s (algorithmic) | % of 8 TB/s |")
+        out.append("|---|---|---|---|---|---|---|---|---|---|")
+        for i, (name, n, k, bias) in enumerate(shapes):
+            mine = gemv[i::len(shapes)]
+            if not mine:
+                continue
+            durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in mine]
+            avg = sum(durs) / len(durs)
+            nbytes = algorithmic_bytes(STEP_QTYPE, n, k, STEP_M, bias)
+            kname = _short_kernel(mine[0]["Kernel_Name"])
+            out.append(f"| {name} {n}x{k} | {kname} | {mine[0]['Grid_Size_X']} | {mine[0]['VGPR_Count']} | "
+                       f"{mine[0]['LDS_Block_Size']} | {len(mine)} | {avg:.2f} | {min(durs):.2f} | "
+                       f"{nbytes / avg / 1e3:.0f} | {nbytes / avg / 1e3 / PEAK_HBM_GBS:.1%} |")
+        if copies:
+            durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in copies]
+            out.append(f"| torch copy 256 MiB | {copies[0]['Kernel_Name'][:40]} | {copies[0]['Grid_Size_X']} | | | "
+                       f"{len(copies)} | {sum(durs) / len(durs):.2f} | {min(durs):.2f} | "
+                       f"{2 * 2**28 / (sum(durs) / len(durs)) / 1e3:.0f} (read+write) | |")
+    for coll in sorted(root.rglob("*counter_collection.csv")):
+        rows = _read_csv(coll)
+        names = sorted({r["Counter_Name"] for r in rows})
+        per = {}
+        for r in rows:
+            per.setdefault(r["Correlation_Id"], {"name": r["Kernel_Name"], "c": {}})
+            per[r["Correlation_Id"]]["c"][r["Counter_Name"]] = (
+                per[r["Correlation_Id"]]["c"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"]))
+        disp = sorted(per.items(), key=lambda kv: int(kv[0]))
+        gemv = [d for _, d in disp if _is_gemv(d["name"])]
+        copies = [d for _, d in disp if "copyBuffer" in d["name"]]
+        out.append("")
+        out.append(f"counters: {coll.relative_to(root)}")
+        out.append("| shape | " + " | ".join(names) + " |")
+        out.append("|---|" + "---|" * len(names))
+        for i, (name, n, k, bias) in enumerate(shapes):
+            mine = gemv[i::len(shapes)]
+            if mine:
+                vals = [sum(d["c"].get(c, 0.0) for d in mine) / len(mine) for c in names]
+                out.append(f"| {name} {n}x{k} | " + " | ".join(f"{v:.6g}" for v in vals) + " |")
+        if copies:
+            vals = [sum(d["c"].get(c, 0.0) for d in copies) / len(copies) for c in names]
+            out.append("| torch copy 256 MiB | " + " | ".join(f"{v:.6g}" for v in vals) + " |")
+    print("\n".join(out))
+
+
 def cpu_baseline(seconds_budget=20.0):
     """The reference's CPU path (tiled fp32 dequantize + F.linear), restated
     in oracle/, for one pass of the step at batch 2, timed on this host."""
@@ -202,7 +302,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--quick", action="store_true", help="skip the sweep and CPU baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--summarize", metavar="DIR",
+                    help="summarize rocprofv3 CSV output of --profile runs under DIR (kernel "
+                         "trace and counter collections) per step GEMV shape, then exit")
+    ap.add_argument("--profile", action="store_true",
+                    help="eager launches for rocprofv3: every step GEMV on 8 copies, twice, then "
+                         "16 torch copies of 256 MiB (the known-size copy that scales FETCH_SIZE "
+                         "and WRITE_SIZE); prints nothing else")
     args = ap.parse_args()
+    if args.summarize:
+        summarize(Path(args.summarize))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(the path runs on one GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
@@ -213,6 +323,9 @@ def main():
     native.load()
     stream = torch.cuda.Stream(dev)
     log(f"device: {torch.cuda.get_device_name(dev)}")
+    if args.profile:
+        profile_pass(dev, stream)
+        return
 
     # --- headline step: 8 passes over the 5 matrices, distinct copies -------
     pool = Pool(dev, q_bytes=3 * 2**30, s_bytes=2**29)

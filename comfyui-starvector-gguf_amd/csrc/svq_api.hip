@@ -6,7 +6,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <map>
 #include <mutex>
+#include <tuple>
 
 #include "../../include/svq.h"
 #include "svq_launch.h"
@@ -40,42 +42,44 @@ bool aligned(const void* p, uintptr_t a) {
   return ((uintptr_t)p & (a - 1)) == 0;
 }
 
-// Launch-shape overrides for tuning sweeps: SVQ_LG_G (log2 lanes per row),
-// SVQ_ROWS (rows per lane group, 1 or 2), SVQ_LDS_KB (LDS budget per
-// workgroup). Read once per process.
+// Launch-shape overrides for tuning sweeps and for tests that exercise both
+// kernels: SVQ_LG_G (log2 lanes per row, 0..6), SVQ_ROWS (rows per lane group,
+// 1 or 2), SVQ_PATH ("stream" or "chunked"), SVQ_LDS_KB (LDS budget of the
+// chunked kernel). Read on every call, so a process may change them.
 struct Tuning {
   int lg_g = -1;
   int rows = 0;
+  int path = 0;  // 0 automatic, 1 streaming, 2 chunked
   int lds_kb = 40;
 };
 
-const Tuning& tuning() {
-  static Tuning t;
-  static std::once_flag once;
-  std::call_once(once, [] {
-    if (const char* v = getenv("SVQ_LG_G")) t.lg_g = atoi(v);
-    if (const char* v = getenv("SVQ_ROWS")) t.rows = atoi(v);
-    if (const char* v = getenv("SVQ_LDS_KB")) t.lds_kb = atoi(v);
-    if (t.lg_g > 6) t.lg_g = 6;
-    if (t.rows != 0 && t.rows != 1 && t.rows != 2) t.rows = 0;
-    if (t.lds_kb < 4 || t.lds_kb > 64) t.lds_kb = 40;
-  });
+Tuning tuning() {
+  Tuning t;
+  if (const char* v = getenv("SVQ_LG_G")) t.lg_g = atoi(v);
+  if (const char* v = getenv("SVQ_ROWS")) t.rows = atoi(v);
+  if (const char* v = getenv("SVQ_PATH"))
+    t.path = strcmp(v, "stream") == 0 ? 1 : strcmp(v, "chunked") == 0 ? 2 : 0;
+  if (const char* v = getenv("SVQ_LDS_KB")) t.lds_kb = atoi(v);
+  if (t.lg_g > 6) t.lg_g = 6;
+  if (t.rows != 0 && t.rows != 1 && t.rows != 2) t.rows = 0;
+  if (t.lds_kb < 4 || t.lds_kb > 64) t.lds_kb = 40;
   return t;
 }
 
-svq::GemvShape choose_shape(int m, int n, int k, int qtype) {
-  const Tuning& tu = tuning();
+// Lanes per row: as many as keep >= 8 units per lane, at most a wave.
+int base_lg_g(int units) {
+  int lg_g = 6;
+  while (lg_g > 0 && (units >> lg_g) < 8) --lg_g;
+  return lg_g;
+}
+
+svq::GemvShape choose_chunked_shape(int m, int n, int k, int qtype, const Tuning& tu) {
   svq::GemvShape sh;
   sh.m = m;
   const int units = (k / 32) * svq::units_per_block(qtype);
-  // Lanes per row: as many as keep >= 8 units per lane, at most a wave.
-  int lg_g = 6;
-  while (lg_g > 0 && (units >> lg_g) < 8) --lg_g;
-  if (tu.lg_g >= 0) lg_g = tu.lg_g;
+  const int lg_g = tu.lg_g >= 0 ? tu.lg_g : base_lg_g(units);
   sh.lg_g = lg_g;
   const int row_groups_per_wave = 64 >> lg_g;
-  // Two rows per lane group halve LDS activation traffic for M >= 2 when
-  // the grid still has >= 2 workgroups per CU of a 256-CU part.
   int rows = 1;
   if (m >= 2 && n / (row_groups_per_wave * 2 * 4) >= 512) rows = 2;
   if (tu.rows) rows = tu.rows;
@@ -87,6 +91,85 @@ svq::GemvShape choose_shape(int m, int n, int k, int qtype) {
   if (chunk < 1) chunk = 1;
   sh.chunk_units = chunk;
   return sh;
+}
+
+// Compute units of the current device and resident waves per CU of a
+// streaming kernel with a given LDS size, cached (host queries only).
+std::mutex g_cache_mu;
+std::map<int, int> g_cus;
+std::map<std::tuple<int, const void*, size_t>, int> g_waves_per_cu;
+
+int device_cus(int dev) {
+  std::lock_guard<std::mutex> lock(g_cache_mu);
+  auto it = g_cus.find(dev);
+  if (it != g_cus.end()) return it->second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  g_cus[dev] = cus;
+  return cus;
+}
+
+int waves_per_cu(int dev, const void* fn, int wpg, size_t lds) {
+  std::lock_guard<std::mutex> lock(g_cache_mu);
+  const auto key = std::make_tuple(dev, fn, lds);
+  auto it = g_waves_per_cu.find(key);
+  if (it != g_waves_per_cu.end()) return it->second;
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, wpg * 64, lds) != hipSuccess ||
+      blocks <= 0)
+    blocks = 1;
+  g_waves_per_cu[key] = blocks * wpg;
+  return blocks * wpg;
+}
+
+constexpr size_t kStreamLdsMax = 156 * 1024;  // nearly all of a CU's 160 KB
+
+// Streaming launch: lanes per row and rows per lane group chosen so that the
+// row tiles cover every resident wave (largest tiles first, which reuse x
+// the most); when there are more tiles than resident waves, the wave count is
+// trimmed so that every wave gets the same number of tiles, as long as that
+// keeps every CU busy. Returns false when x does not fit in LDS or a buffer
+// exceeds the 2^31-byte ranges the kernel addresses.
+bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out,
+                   int* rows_out, int* wpg_out, int* waves_out, int* groups_out) {
+  if (tu.path == 2) return false;
+  const size_t lds = svq::stream_lds_bytes(qtype, m, k);
+  const uint64_t q_bytes = (uint64_t)n * (k / 32) * payload_bytes(qtype);
+  if (lds > kStreamLdsMax || q_bytes >= (1ull << 31) || (uint64_t)n * (k / 16) >= (1ull << 31))
+    return false;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const int cus = device_cus(dev);
+  const int wpg = svq::kStreamWavesPerGroup;
+  const int units = (k / 32) * svq::units_per_block(qtype);
+  const int lg0 = base_lg_g(units);
+  int lg = lg0, rows = 2, wmax = 0, tiles = 0;
+  for (;;) {
+    wmax = cus * waves_per_cu(dev, svq::stream_kernel(qtype, m, rows, wpg), wpg, lds);
+    tiles = (n + ((64 >> lg) * rows) - 1) / ((64 >> lg) * rows);
+    if (tiles >= wmax) break;
+    if (rows == 2) rows = 1;
+    else if (lg < 6) ++lg;
+    else break;
+  }
+  if (tu.lg_g >= 0) lg = tu.lg_g;
+  if (tu.rows) rows = tu.rows;
+  if (tu.lg_g >= 0 || tu.rows) {
+    wmax = cus * waves_per_cu(dev, svq::stream_kernel(qtype, m, rows, wpg), wpg, lds);
+    tiles = (n + ((64 >> lg) * rows) - 1) / ((64 >> lg) * rows);
+  }
+  int waves = tiles < wmax ? tiles : wmax;
+  const int rounds = (tiles + waves - 1) / waves;
+  const int balanced = (tiles + rounds - 1) / rounds;
+  if (balanced >= wmax - wmax / 16) waves = balanced;
+  *lg_out = lg;
+  *rows_out = rows;
+  *wpg_out = wpg;
+  *waves_out = waves;
+  *groups_out = (waves + wpg - 1) / wpg;
+  return true;
 }
 
 }  // namespace
@@ -114,11 +197,12 @@ int svq_gemv(const void* x, const uint8_t* q, const uint16_t* s,
       !aligned(s, 2) || (bias && !aligned(bias, 2)) ||
       !aligned(y, y_dtype == SVQ_F32 ? 4 : 2))
     return fail(SVQ_E_ALIGN, "misaligned pointer (x and q need 16 bytes)");
-  // Per-wave 32-bit offsets: up to 128 rows of payload.
-  if ((uint64_t)(k / 32) * payload_bytes(qtype) * 128 >= (1ull << 32))
+  // Per-wave 32-bit offsets: up to 128 rows of payload stay below 2^31 bytes,
+  // the offset the kernels use for loads that must not touch memory.
+  if ((uint64_t)(k / 32) * payload_bytes(qtype) * 128 >= (1ull << 31))
     return fail(SVQ_E_RANGE, "row of %d weights too long", k);
-  const svq::GemvShape sh = choose_shape(m, n, k, qtype);
-  svq::GemvArgs a;
+  const Tuning tu = tuning();
+  svq::GemvArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.q = q;
   a.s = s;
@@ -126,11 +210,20 @@ int svq_gemv(const void* x, const uint8_t* q, const uint16_t* s,
   a.y = y;
   a.n = n;
   a.k = k;
-  a.lg_g = sh.lg_g;
-  a.chunk_units = sh.chunk_units;
   a.y_f32 = y_dtype == SVQ_F32;
-  const hipError_t e =
-      svq::launch_gemv(a, sh, qtype, static_cast<hipStream_t>(stream));
+  int lg = 0, rows = 0, wpg = 0, waves = 0, groups = 0;
+  hipError_t e;
+  if (choose_stream(m, n, k, qtype, tu, &lg, &rows, &wpg, &waves, &groups)) {
+    a.lg_g = lg;
+    a.waves = waves;
+    e = svq::launch_gemv_stream(a, qtype, m, rows, wpg, groups,
+                                static_cast<hipStream_t>(stream));
+  } else {
+    const svq::GemvShape sh = choose_chunked_shape(m, n, k, qtype, tu);
+    a.lg_g = sh.lg_g;
+    a.chunk_units = sh.chunk_units;
+    e = svq::launch_gemv(a, sh, qtype, static_cast<hipStream_t>(stream));
+  }
   if (e != hipSuccess) return hip_fail(e, "svq_gemv launch");
   return 0;
 }

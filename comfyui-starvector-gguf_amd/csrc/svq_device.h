@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace svq {
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
@@ -254,6 +256,115 @@ __device__ __forceinline__ void load_unit(const uint8_t* p,
     const u32x4 a = *reinterpret_cast<const u32x4*>(p);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
   }
+}
+
+}  // namespace svq
+
+namespace svq {
+
+// Staging of x[:, cu0 : cu0 + cun units] (fp16, all M rows) into LDS in
+// piece-major order, xs[(m * P + p) * stride + u], followed by the per-unit,
+// per-row offset term kSxScale * sum(x over the unit) in sxs[m * stride + u].
+//
+// Split in two so that a kernel can put other loads between them: begin()
+// issues the global loads of the first SB pieces of every thread into
+// registers; finish() writes them to LDS, stages any remaining pieces in
+// batches of SB, computes the offset sums and ends with a barrier. Loads
+// retire in issue order, so loads issued between begin() and finish() (the
+// weight stream) do not delay the first LDS writes. Batch entries past the end
+// re-write the last piece with the same data, so every loaded register is
+// consumed on every path.
+template <int QT, int M, int THREADS, int SB>
+struct XStager {
+  using T = QTraits<QT>;
+  static constexpr int P = T::kUnitWeights / 8;
+  const uint16_t* __restrict__ x;
+  int k, cu0, cun, stride, per_row, total;
+  u32x4 v[SB];
+  int dst[SB];
+
+  __device__ __forceinline__ XStager(const uint16_t* x_, int k_, int cu0_, int cun_, int stride_)
+      : x(x_), k(k_), cu0(cu0_), cun(cun_), stride(stride_), per_row(cun_ * P),
+        total(M * cun_ * P) {}
+
+  __device__ __forceinline__ void load_batch(int base) {
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      int t = min(base + j * THREADS, total - 1);
+      int m = 0;
+      while (t >= per_row) { t -= per_row; ++m; }
+      const int u = t / P, pc = t - u * P;
+      v[j] = reinterpret_cast<const u32x4*>(
+          x + (size_t)m * k + (size_t)cu0 * T::kUnitWeights)[t];
+      dst[j] = (m * P + pc) * stride + u;
+    }
+  }
+
+  __device__ __forceinline__ void store_batch(u32x4* xs) {
+#pragma unroll
+    for (int j = 0; j < SB; ++j) xs[dst[j]] = v[j];
+  }
+
+  __device__ __forceinline__ void begin() { load_batch(threadIdx.x); }
+
+  __device__ __forceinline__ void finish(u32x4* xs, float* sxs) {
+    store_batch(xs);
+    for (int base = threadIdx.x + SB * THREADS; base < total; base += SB * THREADS) {
+      load_batch(base);
+      store_batch(xs);
+    }
+    __syncthreads();
+    const uint32_t ones = 0x3c003c00u;  // fp16 pair (1, 1)
+    for (int t = threadIdx.x; t < M * cun; t += THREADS) {
+      const int m = t / cun, u = t - m * cun;
+      float sx = 0.f;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const u32x4 w = xs[(m * P + p) * stride + u];
+        sx = dot2(w.x, ones, sx);
+        sx = dot2(w.y, ones, sx);
+        sx = dot2(w.z, ones, sx);
+        sx = dot2(w.w, ones, sx);
+      }
+      sxs[m * stride + u] = sx * T::kSxScale;
+    }
+    __syncthreads();
+  }
+};
+
+template <int QT, int M, int THREADS>
+__device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, int k,
+                                        int cu0, int cun, int stride,
+                                        u32x4* xs, float* sxs) {
+  XStager<QT, M, THREADS, 4> st(x, k, cu0, cun, stride);
+  st.begin();
+  st.finish(xs, sxs);
+}
+
+// Sum of v over the G = 1 << lg_g consecutive lanes of a lane group, left in
+// every lane of the group: DPP quad permutes and row mirrors within 16 lanes,
+// then the gfx950 lane-swap instructions across 16- and 32-lane halves. No
+// LDS traffic.
+__device__ __forceinline__ float group_sum(float v, int lg_g) {
+  auto dpp = [](float f, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
+        __builtin_bit_cast(int, f), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  if (lg_g >= 1) v += dpp(v, std::integral_constant<int, 0xb1>{});   // quad_perm [1,0,3,2]
+  if (lg_g >= 2) v += dpp(v, std::integral_constant<int, 0x4e>{});   // quad_perm [2,3,0,1]
+  if (lg_g >= 3) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  if (lg_g >= 4) v += dpp(v, std::integral_constant<int, 0x140>{});  // row_mirror
+  if (lg_g >= 5) {
+    const int i = __builtin_bit_cast(int, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(i, i, false, false);
+    v = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+  }
+  if (lg_g >= 6) {
+    const int i = __builtin_bit_cast(int, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(i, i, false, false);
+    v = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+  }
+  return v;
 }
 
 }  // namespace svq

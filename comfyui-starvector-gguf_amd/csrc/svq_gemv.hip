@@ -16,9 +16,11 @@
 //     LDS budget. While staging, the workgroup also stores for every unit and
 //     activation row offset * sum(x over the unit), the term that removes the
 //     code offset (-8, -16, -128) from the subnormal-code dot products.
-//   * Each lane issues the loads of U units x R rows before using them, to
-//     keep enough HBM requests in flight, then unpacks in registers
-//     (v_perm_b32 into fp16 subnormals) and accumulates with v_dot2_f32_f16.
+//   * Each lane keeps a ring of D units x R rows of payload in flight: slot d
+//     is refilled with the unit D steps ahead as soon as it is unpacked, and
+//     the first D loads go out before the x staging, so the weight stream
+//     never waits on the LDS phase. Units are unpacked in registers
+//     (v_perm_b32 into fp16 subnormals) and accumulated with v_dot2_f32_f16.
 //     A block's dot product is scaled by its fp16 scale once, as the
 //     reference does (quantization.py:199, 215).
 //   * Partial row sums are reduced across the G lanes with cross-lane
@@ -30,8 +32,11 @@ namespace svq {
 
 constexpr int kThreads = 256;
 constexpr int kWavesPerGroup = kThreads / 64;
+// A buffer offset past every per-wave range (the C ABI keeps a wave's rows
+// below 2^31 bytes): loads there return zeros and touch no memory.
+constexpr uint32_t kOutOfRange = 0x80000000u;
 
-template <int QT, int M, int R, int U>
+template <int QT, int M, int R, int D>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   using T = QTraits<QT>;
   constexpr int P = T::kUnitWeights / 8;   // 16-byte activation pieces per unit
@@ -78,65 +83,64 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+  // Bias of the lane's rows, fetched now so its latency overlaps the stream.
+  float bias[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = min(row_lane0 + r, n - 1);
+    bias[r] = a.bias && wave_active ? half_bits_to_float(a.bias[row]) : 0.f;
+  }
 
   const int chunk = a.chunk_units;
   u32x4* xs = lds;
   float* sxs = reinterpret_cast<float*>(lds + M * P * chunk);
-  const uint32_t ones = 0x3c003c00u;  // fp16 pair (1, 1)
+  // Ring of D in-flight units per row: slot d holds the payload dwords and
+  // scale bits of one unit for each of the R rows. Every slot load is issued
+  // unconditionally; a load with nothing to fetch gets an offset past the
+  // buffer's range, which returns zeros without a memory access. (A
+  // conditional load would make the compiler merge register values at the
+  // branch join and wait for the load there.)
+  uint32_t w[D][R][T::kWords];
+  uint32_t sc[D][R];
+  auto load_slot = [&](int d, int cu0, int u, bool valid) {
+    const uint32_t ug = (uint32_t)(cu0 + u);
+    // Added rather than selected: valid offsets are below 2^31, so this moves
+    // an invalid load out of range without giving the compiler a branch.
+    const uint32_t oob = (uint32_t)(!valid) * kOutOfRange;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      load_unit_buf<QT>(qr, qoff[r] + ug * T::kUnitBytes + oob, w[d][r]);
+      sc[d][r] = __builtin_amdgcn_raw_buffer_load_b16(
+          sr, soff[r] + (ug / T::kUnitsPerBlock) * 2u + oob, 0, 0);
+    }
+  };
 
   for (int cu0 = 0; cu0 < units; cu0 += chunk) {
     const int cun = min(chunk, units - cu0);
-    if (cu0 > 0) __syncthreads();  // previous chunk fully consumed
-    // Stage x[:, chunk] into LDS. Consecutive threads read consecutive
-    // 16-byte pieces of a row of x.
-    for (int m = 0; m < M; ++m) {
-      const u32x4* xrow = reinterpret_cast<const u32x4*>(
-          a.x + (size_t)m * k + (size_t)cu0 * T::kUnitWeights);
-      for (int t = threadIdx.x; t < cun * P; t += kThreads) {
-        const int u = t / P, p = t - u * P;
-        xs[(m * P + p) * chunk + u] = xrow[t];
-      }
-    }
-    __syncthreads();
-    for (int t = threadIdx.x; t < M * cun; t += kThreads) {
-      const int m = t / cun, u = t - m * cun;
-      float sx = 0.f;
+    // Units of this chunk handled by this lane: g, g + G, ...
+    const int niter = g < cun ? (cun - g + G - 1) >> lg_g : 0;
+    // The first D loads are issued before the x staging and its barriers, so
+    // the two memory latencies overlap.
+    if (wave_active) {
 #pragma unroll
-      for (int p = 0; p < P; ++p) {
-        const u32x4 v = xs[(m * P + p) * chunk + u];
-        sx = dot2(v.x, ones, sx);
-        sx = dot2(v.y, ones, sx);
-        sx = dot2(v.z, ones, sx);
-        sx = dot2(v.w, ones, sx);
-      }
-      sxs[m * chunk + u] = sx * T::kSxScale;
+      for (int d = 0; d < D; ++d) load_slot(d, cu0, g + d * G, d < niter);
     }
-    __syncthreads();
+    if (cu0 > 0) __syncthreads();  // previous chunk fully consumed
+    stage_x<QT, M, kThreads>(a.x, k, cu0, cun, chunk, xs, sxs);
 
     if (wave_active) {
-      for (int u0 = g; u0 < cun; u0 += G * U) {
-        uint32_t w[U][R][T::kWords];
-        uint32_t sc[U][R];
-        // Issue every load of this step before any use; units past the chunk
-        // end re-read the chunk's last unit and are skipped below.
+      for (int i = 0; i < niter; i += D) {
 #pragma unroll
-        for (int uu = 0; uu < U; ++uu) {
-          const int u = min(u0 + uu * G, cun - 1);
-          const uint32_t ug = (uint32_t)(cu0 + u);
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            load_unit_buf<QT>(qr, qoff[r] + ug * T::kUnitBytes, w[uu][r]);
-            sc[uu][r] = __builtin_amdgcn_raw_buffer_load_b16(
-                sr, soff[r] + (ug / T::kUnitsPerBlock) * 2u, 0, 0);
-          }
-        }
-#pragma unroll
-        for (int uu = 0; uu < U; ++uu) {
-          const int u = u0 + uu * G;
-          if (u < cun) {
+        for (int d = 0; d < D; ++d) {
+          const int it = i + d;
+          const int u = g + it * G;
+          if (it < niter) {
             uint32_t pk[R][XW];
 #pragma unroll
-            for (int r = 0; r < R; ++r) unpack<QT>(w[uu][r], pk[r]);
+            for (int r = 0; r < R; ++r) unpack<QT>(w[d][r], pk[r]);
+            float dsc[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) dsc[r] = half_bits_to_float((uint16_t)sc[d][r]);
 #pragma unroll
             for (int m = 0; m < M; ++m) {
               uint32_t xv[XW];
@@ -148,13 +152,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
               }
               const float off = sxs[m * chunk + u];
 #pragma unroll
-              for (int r = 0; r < R; ++r) {
-                const float t = unit_dot<QT>(pk[r], xv, off);
-                acc[r][m] = __builtin_fmaf(
-                    t, half_bits_to_float((uint16_t)sc[uu][r]), acc[r][m]);
-              }
+              for (int r = 0; r < R; ++r)
+                acc[r][m] = __builtin_fmaf(unit_dot<QT>(pk[r], xv, off), dsc[r], acc[r][m]);
             }
           }
+          // Refill the slot with the unit D steps ahead.
+          load_slot(d, cu0, u + D * G, it + D < niter);
         }
       }
     }
@@ -175,10 +178,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   for (int r = 0; r < R; ++r) {
     const int row = row_lane0 + r;
     if (row >= n) break;
-    const float b = a.bias ? half_bits_to_float(a.bias[row]) : 0.f;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const float v = __builtin_fmaf(acc[r][m], T::kOutScale, b);
+      const float v = __builtin_fmaf(acc[r][m], T::kOutScale, bias[r]);
       if (a.y_f32)
         reinterpret_cast<float*>(a.y)[(size_t)m * n + row] = v;
       else
@@ -191,11 +193,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 template <int QT>
 constexpr int lds_unit_bytes() { return QTraits<QT>::kUnitWeights * 2 + 4; }
 
-template <int QT, int M, int R, int U>
+template <int QT, int M, int R, int D>
 static hipError_t launch_one(const GemvArgs& a, const GemvShape& sh,
                              hipStream_t stream) {
   const size_t lds = (size_t)M * sh.chunk_units * lds_unit_bytes<QT>();
-  hipLaunchKernelGGL((gemv_kernel<QT, M, R, U>), dim3(sh.groups),
+  hipLaunchKernelGGL((gemv_kernel<QT, M, R, D>), dim3(sh.groups),
                      dim3(kThreads), lds, stream, a);
   return hipGetLastError();
 }
@@ -203,8 +205,8 @@ static hipError_t launch_one(const GemvArgs& a, const GemvShape& sh,
 template <int QT, int M>
 static hipError_t launch_m(const GemvArgs& a, const GemvShape& sh,
                            hipStream_t stream) {
-  if (sh.rows_per_group == 2) return launch_one<QT, M, 2, 2>(a, sh, stream);
-  return launch_one<QT, M, 1, 4>(a, sh, stream);
+  if (sh.rows_per_group == 2) return launch_one<QT, M, 2, 4>(a, sh, stream);
+  return launch_one<QT, M, 1, 8>(a, sh, stream);
 }
 
 template <int QT>

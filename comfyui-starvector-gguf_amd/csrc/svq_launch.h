@@ -14,8 +14,9 @@ struct GemvArgs {
   void* y;               // [m, n] fp16 or fp32
   int n, k;
   int lg_g;         // log2 of the lanes that share a row
-  int chunk_units;  // units of x staged in LDS at a time
+  int chunk_units;  // units of x staged in LDS at a time (chunked kernel)
   int y_f32;
+  int waves;        // streaming waves in the grid (streaming kernel)
 };
 
 struct GemvShape {
@@ -31,6 +32,15 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvShape& sh, int qtype,
                        hipStream_t stream);
 int lds_bytes_per_unit(int qtype);
 int units_per_block(int qtype);
+
+// Streaming kernel (svq_gemv_stream.hip): waves per workgroup, LDS bytes it
+// needs for x and the offset sums, its function pointer (for occupancy
+// queries) and launcher.
+constexpr int kStreamWavesPerGroup = 4;
+size_t stream_lds_bytes(int qtype, int m, int k);
+const void* stream_kernel(int qtype, int m, int rows, int wpg);
+hipError_t launch_gemv_stream(const GemvArgs& a, int qtype, int m, int rows, int wpg,
+                              int groups, hipStream_t stream);
 
 hipError_t launch_dequant(const uint8_t* q, const uint16_t* s, void* out,
                           int64_t nblocks, int qtype, int out_dtype,

@@ -252,3 +252,46 @@ def test_gemv_fp16_denormal_activations(cuda_device):
     y = hip_gemv(to_dev(x, cuda_device), to_dev(q, cuda_device), to_dev(s, cuda_device), "Q5_0", n,
                  None, torch.float32)
     assert orc.rel_err(y.cpu().numpy(), ref) <= FP32_TOL
+
+
+@pytest.fixture
+def kernel_path(request, monkeypatch):
+    """Force the streaming or the chunked GEMV kernel (read per call)."""
+    monkeypatch.setenv("SVQ_PATH", request.param)
+    return request.param
+
+
+@pytest.mark.parametrize("kernel_path", ["stream", "chunked"], indirect=True)
+@pytest.mark.parametrize("qtype", QTYPES)
+def test_gemv_both_kernels_against_oracle(cuda_device, kernel_path, qtype):
+    rng = np.random.default_rng(7)
+    for m in (1, 2, 3, 8):
+        for n, k in ((1, 32), (13, 128), (33, 192), (129, 2048), (515, 4608), (40, 18432)):
+            say(f"gemv {kernel_path} {qtype} m={m} n={n} k={k}")
+            q, s = orc.synthetic_soa(qtype, n, k, seed=n + k + m)
+            x = rng.standard_normal((m, k)).astype(np.float16)
+            bias = rng.standard_normal(n).astype(np.float16)
+            ref = orc.gemv_ref(x, q, s, qtype, n, k, bias)
+            y = hip_gemv(to_dev(x, cuda_device), to_dev(q, cuda_device), to_dev(s, cuda_device), qtype, n,
+                         to_dev(bias, cuda_device), torch.float32)
+            assert orc.rel_err(y.cpu().numpy(), ref) <= FP32_TOL, (kernel_path, m, n, k)
+
+
+@pytest.mark.parametrize("lg_g", range(0, 7))
+@pytest.mark.parametrize("rows", (1, 2))
+def test_gemv_every_launch_shape(cuda_device, monkeypatch, lg_g, rows):
+    """Every lanes-per-row / rows-per-group choice, on ragged shapes."""
+    monkeypatch.setenv("SVQ_LG_G", str(lg_g))
+    monkeypatch.setenv("SVQ_ROWS", str(rows))
+    rng = np.random.default_rng(lg_g * 10 + rows)
+    for path in ("stream", "chunked"):
+        monkeypatch.setenv("SVQ_PATH", path)
+        for qtype in QTYPES:
+            for m, n, k in ((1, 77, 320), (2, 130, 1056), (5, 3, 96)):
+                say(f"gemv shape lg_g={lg_g} rows={rows} {path} {qtype} m={m} n={n} k={k}")
+                q, s = orc.synthetic_soa(qtype, n, k, seed=m * n + k)
+                x = rng.standard_normal((m, k)).astype(np.float16)
+                ref = orc.gemv_ref(x, q, s, qtype, n, k)
+                y = hip_gemv(to_dev(x, cuda_device), to_dev(q, cuda_device), to_dev(s, cuda_device), qtype,
+                             n, None, torch.float32)
+                assert orc.rel_err(y.cpu().numpy(), ref) <= FP32_TOL, (lg_g, rows, path, qtype, m, n, k)
