@@ -206,63 +206,134 @@ def _read_csv(path):
         return list(csv.DictReader(f))
 
 
-def summarize(root: Path):
-    """Per-shape averages from rocprofv3 CSVs of `bench.py --profile` runs.
+def _durations_us(rows):
+    return [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows]
 
-    GEMV dispatches are mapped to shapes by their order (the profile pass
-    launches the step shapes round-robin); the torch copy of 256 MiB is the
-    known-size kernel whose FETCH_SIZE / WRITE_SIZE give the counters' scale.
+
+def _counter_dispatches(path):
+    """{correlation id: (kernel name, {counter: value summed over its instances})}, in order."""
+    per = {}
+    for r in _read_csv(path):
+        name, c = per.setdefault(r["Correlation_Id"], (r["Kernel_Name"], {}))
+        c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return [per[key] for key in sorted(per, key=int)]
+
+
+def summarize(root: Path):
+    """Tables from rocprofv3 CSV output found under `root`.
+
+    * A kernel trace of `bench.py --profile` (two eager passes of the step on
+      8 weight copies) is tabulated per step shape: GEMV dispatches are mapped
+      to shapes by their launch order. Any other kernel trace (for instance
+      of the plain bench command) is grouped by kernel, grid and LDS size.
+    * Counter collections of `bench.py --profile` are averaged per shape. The
+      torch copy of 256 MiB is the plain copy kernel of known size: FETCH_SIZE
+      and WRITE_SIZE (KiB per dispatch) are scaled by 256 MiB / what the copy
+      reads for them, and a "traffic" line per shape gives the HBM bytes per
+      launch that result, next to the algorithmic bytes.
     """
-    shapes = [(name, n, k, bias) for name, n, k, bias in STEP_SHAPES]
+    shapes = list(STEP_SHAPES)
+    profile_dispatches = 2 * COPIES * len(shapes)
+    copy_kib = 2**28 / 1024
     out = []
-    traces = sorted(root.rglob("*kernel_trace.csv"))
-    if traces:
-        rows = _read_csv(traces[0])
+    for trace in sorted(root.rglob("*kernel_trace.csv")):
+        # Rows are written as dispatches complete; launch order is Dispatch_Id.
+        rows = sorted(_read_csv(trace), key=lambda r: int(r["Dispatch_Id"]))
         gemv = [r for r in rows if _is_gemv(r["Kernel_Name"])]
         copies = [r for r in rows if "copyBuffer" in r["Kernel_Name"]]
-        out.append(f"kernel trace: {traces[0].relative_to(root)} ({len(gemv)} GEMV dispatches)")
-        out.append("| shape | kernel | grid | VGPR | LDS B | dispatches | avg us | min us | GB/s (algorithmic) | % of 8 TB/s |")
-        out.append("|---|---|---|---|---|---|---|---|---|---|")
-        for i, (name, n, k, bias) in enumerate(shapes):
-            mine = gemv[i::len(shapes)]
-            if not mine:
-                continue
-            durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in mine]
-            avg = sum(durs) / len(durs)
-            nbytes = algorithmic_bytes(STEP_QTYPE, n, k, STEP_M, bias)
-            kname = _short_kernel(mine[0]["Kernel_Name"])
-            out.append(f"| {name} {n}x{k} | {kname} | {mine[0]['Grid_Size_X']} | {mine[0]['VGPR_Count']} | "
-                       f"{mine[0]['LDS_Block_Size']} | {len(mine)} | {avg:.2f} | {min(durs):.2f} | "
-                       f"{nbytes / avg / 1e3:.0f} | {nbytes / avg / 1e3 / PEAK_HBM_GBS:.1%} |")
-        if copies:
-            durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in copies]
-            out.append(f"| torch copy 256 MiB | {copies[0]['Kernel_Name'][:40]} | {copies[0]['Grid_Size_X']} | | | "
-                       f"{len(copies)} | {sum(durs) / len(durs):.2f} | {min(durs):.2f} | "
-                       f"{2 * 2**28 / (sum(durs) / len(durs)) / 1e3:.0f} (read+write) | |")
-    for coll in sorted(root.rglob("*counter_collection.csv")):
-        rows = _read_csv(coll)
-        names = sorted({r["Counter_Name"] for r in rows})
-        per = {}
-        for r in rows:
-            per.setdefault(r["Correlation_Id"], {"name": r["Kernel_Name"], "c": {}})
-            per[r["Correlation_Id"]]["c"][r["Counter_Name"]] = (
-                per[r["Correlation_Id"]]["c"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"]))
-        disp = sorted(per.items(), key=lambda kv: int(kv[0]))
-        gemv = [d for _, d in disp if _is_gemv(d["name"])]
-        copies = [d for _, d in disp if "copyBuffer" in d["name"]]
+        out.append(f"kernel trace: {trace.relative_to(root)} ({len(gemv)} GEMV dispatches)")
+        if len(gemv) == profile_dispatches:
+            out.append("| shape | kernel | grid | VGPR | LDS B | dispatches | avg us | min us "
+                       "| GB/s (algorithmic) | % of 8 TB/s |")
+            out.append("|---|---|---|---|---|---|---|---|---|---|")
+            for i, (name, n, k, bias) in enumerate(shapes):
+                mine = gemv[i::len(shapes)]
+                durs = _durations_us(mine)
+                avg = sum(durs) / len(durs)
+                nbytes = algorithmic_bytes(STEP_QTYPE, n, k, STEP_M, bias)
+                out.append(f"| {name} {n}x{k} | {_short_kernel(mine[0]['Kernel_Name'])} | "
+                           f"{mine[0]['Grid_Size_X']} | {mine[0]['VGPR_Count']} | "
+                           f"{mine[0]['LDS_Block_Size']} | {len(mine)} | {avg:.2f} | {min(durs):.2f} | "
+                           f"{nbytes / avg / 1e3:.0f} | {nbytes / avg / 1e3 / PEAK_HBM_GBS:.1%} |")
+        else:
+            groups = {}
+            for r in gemv:
+                key = (_short_kernel(r["Kernel_Name"]), r["Grid_Size_X"], r["LDS_Block_Size"])
+                groups.setdefault(key, []).append(r)
+            out.append("| kernel | grid | LDS B | dispatches | avg us | min us | max us |")
+            out.append("|---|---|---|---|---|---|---|")
+            for (kname, grid, lds), mine in groups.items():
+                durs = _durations_us(mine)
+                out.append(f"| {kname} | {grid} | {lds} | {len(mine)} | {sum(durs) / len(durs):.2f} | "
+                           f"{min(durs):.2f} | {max(durs):.2f} |")
+        if copies and len(gemv) == profile_dispatches:
+            durs = _durations_us(copies)
+            out.append(f"| torch copy 256 MiB | {copies[0]['Grid_Size_X']} | | {len(copies)} | "
+                       f"{sum(durs) / len(durs):.2f} | {min(durs):.2f} | "
+                       f"{2 * 2**28 / (sum(durs) / len(durs)) / 1e3:.0f} GB/s read+write |")
         out.append("")
+    for stats in sorted(root.rglob("*kernel_stats.csv")):
+        out.append(f"kernel stats (rocprofv3 --stats): {stats.relative_to(root)}")
+        out.append("| kernel | calls | avg us | min us | max us | % of GPU time |")
+        out.append("|---|---|---|---|---|---|")
+        for r in _read_csv(stats):
+            if _is_gemv(r["Name"]) or "copyBuffer" in r["Name"]:
+                out.append(f"| {_short_kernel(r['Name'])} | {r['Calls']} | "
+                           f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                           f"{float(r['MaxNs']) / 1e3:.2f} | {r['Percentage']} |")
+        out.append("")
+    per_shape = {}   # shape name -> {counter: average per dispatch}
+    scale = {}       # counter -> bytes per unit the counter reports
+    for coll in sorted(root.rglob("*counter_collection.csv")):
+        disp = _counter_dispatches(coll)
+        gemv = [c for name, c in disp if _is_gemv(name)]
+        copies = [c for name, c in disp if "copyBuffer" in name]
+        names = sorted({n for c in gemv + copies for n in c})
         out.append(f"counters: {coll.relative_to(root)}")
         out.append("| shape | " + " | ".join(names) + " |")
         out.append("|---|" + "---|" * len(names))
-        for i, (name, n, k, bias) in enumerate(shapes):
-            mine = gemv[i::len(shapes)]
-            if mine:
-                vals = [sum(d["c"].get(c, 0.0) for d in mine) / len(mine) for c in names]
-                out.append(f"| {name} {n}x{k} | " + " | ".join(f"{v:.6g}" for v in vals) + " |")
+        if len(gemv) == profile_dispatches:
+            for i, (name, n, k, bias) in enumerate(shapes):
+                mine = gemv[i::len(shapes)]
+                vals = {c: sum(d.get(c, 0.0) for d in mine) / len(mine) for c in names}
+                per_shape.setdefault(name, {}).update(vals)
+                out.append(f"| {name} {n}x{k} | " + " | ".join(f"{vals[c]:.6g}" for c in names) + " |")
         if copies:
-            vals = [sum(d["c"].get(c, 0.0) for d in copies) / len(copies) for c in names]
-            out.append("| torch copy 256 MiB | " + " | ".join(f"{v:.6g}" for v in vals) + " |")
+            vals = {c: sum(d.get(c, 0.0) for d in copies) / len(copies) for c in names}
+            out.append("| torch copy 256 MiB | " + " | ".join(f"{vals[c]:.6g}" for c in names) + " |")
+            for c in ("FETCH_SIZE", "WRITE_SIZE"):
+                if vals.get(c):
+                    scale[c] = copy_kib * 1024 / vals[c]
+        out.append("")
+    if "FETCH_SIZE" in scale and "WRITE_SIZE" in scale:
+        out.append(f"copy scale: FETCH_SIZE x {scale['FETCH_SIZE']:.1f} B, "
+                   f"WRITE_SIZE x {scale['WRITE_SIZE']:.1f} B (256 MiB copy = 268435456 B each way)")
+        for name, n, k, bias in shapes:
+            c = per_shape.get(name, {})
+            if "FETCH_SIZE" in c and "WRITE_SIZE" in c:
+                rd = c["FETCH_SIZE"] * scale["FETCH_SIZE"]
+                wr = c["WRITE_SIZE"] * scale["WRITE_SIZE"]
+                alg = algorithmic_bytes(STEP_QTYPE, n, k, STEP_M, bias)
+                out.append(f"traffic {name} {n}x{k}: {rd + wr:.0f} B per launch "
+                           f"(read {rd:.0f}, write {wr:.0f}; algorithmic {alg}; "
+                           f"ratio {(rd + wr) / alg:.3f})")
     print("\n".join(out))
+
+
+TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_q5_0_m2_8b_step_counters.md"
+
+
+def committed_traffic(name, n, k):
+    """HBM bytes per launch of one step shape, read from the committed
+    FETCH_SIZE / WRITE_SIZE summary (the "traffic" lines `--summarize` writes),
+    or None when that summary is absent."""
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    tag = f"traffic {name} {n}x{k}: "
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if line.startswith(tag):
+            return int(line[len(tag):].split()[0])
+    return None
 
 
 def cpu_baseline(seconds_budget=20.0):
@@ -366,8 +437,9 @@ def main():
     achieved = head_bytes / (head_ms * 1e-3) / 1e9
     del hgraph
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                "kernel": f"svq gemv_kernel {STEP_QTYPE} M={STEP_M} lm_head {hn}x{hk}",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": committed_traffic(hname, hn, hk),
+                "traffic_source": TRAFFIC_SUMMARY.name,
+                "kernel": f"svq gemv_stream_kernel {STEP_QTYPE} M={STEP_M} lm_head {hn}x{hk}",
                 "us_per_launch": round(head_ms * 1e3, 2), "bytes_per_launch": head_bytes}
     log(f"lm_head: {head_ms * 1e3:.2f} us, {achieved:.1f} GB/s")
 

@@ -52,6 +52,8 @@ def load() -> ctypes.CDLL:
         lib.svq_last_error.restype = ctypes.c_char_p
         lib.svq_gemv.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
         lib.svq_gemv.restype = i32
+        lib.svq_gemv_plan.argtypes = [i32, i32, i32, i32, ctypes.POINTER(ctypes.c_int32)]
+        lib.svq_gemv_plan.restype = i32
         lib.svq_dequant.argtypes = [vp, vp, vp, i64, i32, i32, vp]
         lib.svq_dequant.restype = i32
         lib.svq_dequant_rows.argtypes = [vp, vp, vp, i64, i64, i32, vp, i32, i32, vp]
@@ -101,6 +103,20 @@ def gemv(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, y: torch.Tensor,
                           m, n, k, QTYPE_CODE[qtype], DTYPE_CODE[y.dtype],
                           _stream(x.device))
     _check(lib, "svq_gemv", rc)
+
+
+PLAN_FIELDS = ("kernel", "lg_g", "rows", "waves_per_group", "waves", "groups",
+               "wave_capacity", "chunk_units")
+
+
+def gemv_plan(m: int, n: int, k: int, qtype: str) -> dict:
+    """The launch svq_gemv would make for this shape on the current device."""
+    lib = load()
+    out = (ctypes.c_int32 * 8)()
+    _check(lib, "svq_gemv_plan", lib.svq_gemv_plan(m, n, k, QTYPE_CODE[qtype], out))
+    plan = dict(zip(PLAN_FIELDS, list(out)))
+    plan["kernel"] = {1: "stream", 2: "chunked"}[plan["kernel"]]
+    return plan
 
 
 def dequant(q: torch.Tensor, s: torch.Tensor, out: torch.Tensor, qtype: str) -> None:

@@ -133,7 +133,8 @@ constexpr size_t kStreamLdsMax = 156 * 1024;  // nearly all of a CU's 160 KB
 // keeps every CU busy. Returns false when x does not fit in LDS or a buffer
 // exceeds the 2^31-byte ranges the kernel addresses.
 bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out,
-                   int* rows_out, int* wpg_out, int* waves_out, int* groups_out) {
+                   int* rows_out, int* wpg_out, int* waves_out, int* groups_out,
+                   int* wmax_out = nullptr) {
   if (tu.path == 2) return false;
   const size_t lds = svq::stream_lds_bytes(qtype, m, k);
   const uint64_t q_bytes = (uint64_t)n * (k / 32) * payload_bytes(qtype);
@@ -169,6 +170,7 @@ bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out
   *wpg_out = wpg;
   *waves_out = waves;
   *groups_out = (waves + wpg - 1) / wpg;
+  if (wmax_out) *wmax_out = wmax;
   return true;
 }
 
@@ -225,6 +227,26 @@ int svq_gemv(const void* x, const uint8_t* q, const uint16_t* s,
     e = svq::launch_gemv(a, sh, qtype, static_cast<hipStream_t>(stream));
   }
   if (e != hipSuccess) return hip_fail(e, "svq_gemv launch");
+  return 0;
+}
+
+int svq_gemv_plan(int m, int n, int k, int qtype, int32_t* plan) {
+  if (!valid_qtype(qtype)) return fail(SVQ_E_QTYPE, "unsupported qtype %d", qtype);
+  if (m < 1 || m > SVQ_MAX_ROWS || n < 1 || k < 32 || k % 32)
+    return fail(SVQ_E_SHAPE, "invalid shape m=%d n=%d k=%d", m, n, k);
+  if (!plan) return fail(SVQ_E_NULL, "NULL plan");
+  const Tuning tu = tuning();
+  int lg = 0, rows = 0, wpg = 0, waves = 0, groups = 0, wmax = 0;
+  for (int i = 0; i < 8; ++i) plan[i] = 0;
+  if (choose_stream(m, n, k, qtype, tu, &lg, &rows, &wpg, &waves, &groups, &wmax)) {
+    const int32_t p[8] = {1, lg, rows, wpg, waves, groups, wmax, 0};
+    for (int i = 0; i < 8; ++i) plan[i] = p[i];
+  } else {
+    const svq::GemvShape sh = choose_chunked_shape(m, n, k, qtype, tu);
+    const int32_t p[8] = {2, sh.lg_g, sh.rows_per_group, 4, sh.groups * 4, sh.groups, 0,
+                          sh.chunk_units};
+    for (int i = 0; i < 8; ++i) plan[i] = p[i];
+  }
   return 0;
 }
 

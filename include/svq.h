@@ -80,6 +80,17 @@ int svq_gemv(const void *x, const uint8_t *q, const uint16_t *s,
              int y_dtype, void *stream);
 
 /*
+ * Diagnostic with no counterpart in the reference (whose launch tuple is the
+ * per-(qtype, M) table SOA_GEMV_CONFIG, quantization.py:121-127): the launch
+ * svq_gemv would make for this shape on the current device, as
+ * plan[0..7] = {kernel (1 streaming, 2 chunked), log2 lanes per row,
+ * rows per lane group, waves per workgroup, waves, workgroups,
+ * resident-wave capacity used for the choice, chunk units (chunked only)}.
+ * Queries device attributes; launches nothing.
+ */
+int svq_gemv_plan(int m, int n, int k, int qtype, int32_t *plan);
+
+/*
  * out[b * 32 + j] = weight j of block b, for b < nblocks, rounded from the
  * exact fp32 product to out_dtype (SVQ_F32 / SVQ_F16 / SVQ_BF16, round to
  * nearest even). Replaces `dequantize_soa` (quantization.py:93-105) on the GPU.

@@ -95,3 +95,13 @@ def test_dequant_rows_rejects_bad_arguments():
 def test_error_message_names_the_problem():
     gemv(m=11)
     assert "m=11" in native.load().svq_last_error().decode()
+
+
+def test_gemv_plan_rejects_bad_arguments():
+    lib = native.load()
+    plan = (ctypes.c_int32 * 8)()
+    assert lib.svq_gemv_plan(2, 64, 64, 3, plan) == -1
+    assert lib.svq_gemv_plan(9, 64, 64, 4, plan) == -2
+    assert lib.svq_gemv_plan(2, 64, 40, 4, plan) == -2
+    assert lib.svq_gemv_plan(2, 0, 64, 4, plan) == -2
+    assert lib.svq_gemv_plan(2, 64, 64, 4, None) == -3
