@@ -42,15 +42,19 @@ bool aligned(const void* p, uintptr_t a) {
   return ((uintptr_t)p & (a - 1)) == 0;
 }
 
-// Launch-shape overrides for tuning sweeps and for tests that exercise both
-// kernels: SVQ_LG_G (log2 lanes per row, 0..6), SVQ_ROWS (rows per lane group,
-// 1 or 2), SVQ_PATH ("stream" or "chunked"), SVQ_LDS_KB (LDS budget of the
-// chunked kernel). Read on every call, so a process may change them.
+// Launch-shape overrides for tuning sweeps and for tests that exercise every
+// kernel: SVQ_PATH ("mfma", "stream" or "chunked"), SVQ_LG_G (log2 lanes per
+// row, 0..6) and SVQ_ROWS (rows per lane group, 1 or 2) of the streaming and
+// chunked kernels, SVQ_LDS_KB (LDS budget of the chunked kernel), and
+// SVQ_MFMA_R (16-row tiles per wave, 1 or 2), SVQ_MFMA_S (K splits, 1..16) and
+// SVQ_MFMA_P (tile slots per workgroup) of the MFMA kernel. Read on every
+// call, so a process may change them.
 struct Tuning {
   int lg_g = -1;
   int rows = 0;
-  int path = 0;  // 0 automatic, 1 streaming, 2 chunked
+  int path = 0;  // 0 automatic, 1 streaming, 2 chunked, 3 mfma
   int lds_kb = 40;
+  int mfma_r = 0, mfma_s = 0, mfma_p = 0;
 };
 
 Tuning tuning() {
@@ -58,11 +62,20 @@ Tuning tuning() {
   if (const char* v = getenv("SVQ_LG_G")) t.lg_g = atoi(v);
   if (const char* v = getenv("SVQ_ROWS")) t.rows = atoi(v);
   if (const char* v = getenv("SVQ_PATH"))
-    t.path = strcmp(v, "stream") == 0 ? 1 : strcmp(v, "chunked") == 0 ? 2 : 0;
+    t.path = strcmp(v, "stream") == 0    ? 1
+             : strcmp(v, "chunked") == 0 ? 2
+             : strcmp(v, "mfma") == 0    ? 3
+                                         : 0;
   if (const char* v = getenv("SVQ_LDS_KB")) t.lds_kb = atoi(v);
+  if (const char* v = getenv("SVQ_MFMA_R")) t.mfma_r = atoi(v);
+  if (const char* v = getenv("SVQ_MFMA_S")) t.mfma_s = atoi(v);
+  if (const char* v = getenv("SVQ_MFMA_P")) t.mfma_p = atoi(v);
   if (t.lg_g > 6) t.lg_g = 6;
   if (t.rows != 0 && t.rows != 1 && t.rows != 2) t.rows = 0;
   if (t.lds_kb < 4 || t.lds_kb > 64) t.lds_kb = 40;
+  if (t.mfma_r != 1 && t.mfma_r != 2) t.mfma_r = 0;
+  if (t.mfma_s < 0 || t.mfma_s > 16) t.mfma_s = 0;
+  if (t.mfma_p < 0 || t.mfma_p > 16) t.mfma_p = 0;
   return t;
 }
 
@@ -97,7 +110,7 @@ svq::GemvShape choose_chunked_shape(int m, int n, int k, int qtype, const Tuning
 // streaming kernel with a given LDS size, cached (host queries only).
 std::mutex g_cache_mu;
 std::map<int, int> g_cus;
-std::map<std::tuple<int, const void*, size_t>, int> g_waves_per_cu;
+std::map<std::tuple<int, const void*, int, size_t>, int> g_waves_per_cu;
 
 int device_cus(int dev) {
   std::lock_guard<std::mutex> lock(g_cache_mu);
@@ -113,7 +126,7 @@ int device_cus(int dev) {
 
 int waves_per_cu(int dev, const void* fn, int wpg, size_t lds) {
   std::lock_guard<std::mutex> lock(g_cache_mu);
-  const auto key = std::make_tuple(dev, fn, lds);
+  const auto key = std::make_tuple(dev, fn, wpg, lds);
   auto it = g_waves_per_cu.find(key);
   if (it != g_waves_per_cu.end()) return it->second;
   int blocks = 0;
@@ -174,6 +187,59 @@ bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out
   return true;
 }
 
+constexpr int kMfmaMinRows = 5;  // smallest M sent to the MFMA kernel by default
+
+// MFMA launch: 16-row tiles, split along K until tiles x splits give about
+// 16 waves per CU (each split keeping >= 2 steps), persistent workgroups
+// trimmed so that each processes the same number of tile groups. Returns false
+// when the shape or alignment does not suit the kernel: K must be a whole
+// number of steps (4 blocks, 2 for Q8_0), the scales 4-byte aligned, x and
+// its offset sums must fit in LDS, and the arrays below 2^31 bytes.
+bool choose_mfma(int m, int n, int k, int qtype, const Tuning& tu, const void* s, int* rows_out,
+                 int* slots_out, int* ksplit_out, int* groups_out) {
+  if (tu.path == 1 || tu.path == 2) return false;
+  // Automatic choice: the matrix cores pay off once the per-weight dot work
+  // (M fp32 FMAs per weight on the vector path) outweighs the MFMA path's
+  // fixed cost; measured crossover at MI355X decoder shapes is M = 4..5.
+  if (tu.path == 0 && m < kMfmaMinRows) return false;
+  const int kb = k / 32;
+  const int bps = svq::mfma_blocks_per_step(qtype);
+  if (kb % bps || !aligned(s, 4)) return false;
+  const int steps = kb / bps;
+  const uint64_t q_bytes = (uint64_t)n * kb * payload_bytes(qtype);
+  if (q_bytes >= (1ull << 31) || (uint64_t)n * kb * 2 >= (1ull << 31)) return false;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const int cus = device_cus(dev);
+  const int rows = tu.mfma_r ? tu.mfma_r : (m >= kMfmaMinRows ? 2 : 1);
+  const int tiles = (n + 16 * rows - 1) / (16 * rows);
+  int ksplit = 1;
+  if (tu.mfma_s) {
+    ksplit = tu.mfma_s;
+  } else {
+    while (ksplit < 16 && (int64_t)tiles * 2 * ksplit <= (int64_t)cus * 16 &&
+           steps >= 4 * ksplit)
+      ksplit *= 2;
+  }
+  if (ksplit > steps) ksplit = steps;  // every wave needs at least one step
+  int slots = tu.mfma_p ? tu.mfma_p : (ksplit >= 4 ? 1 : 4 / ksplit);
+  if (slots * ksplit > 16) slots = 16 / ksplit;
+  if (slots < 1) return false;
+  const int wpg = slots * ksplit;
+  const size_t lds = svq::mfma_lds_bytes(qtype, m, k, rows, wpg, ksplit);
+  if (lds > kStreamLdsMax) return false;
+  const int per_cu = waves_per_cu(dev, svq::mfma_kernel(qtype, m, rows), wpg, lds) / wpg;
+  const int tile_groups = (tiles + slots - 1) / slots;
+  int groups = tile_groups < cus * per_cu ? tile_groups : cus * per_cu;
+  const int rounds = (tile_groups + groups - 1) / groups;
+  groups = (tile_groups + rounds - 1) / rounds;
+  *rows_out = rows;
+  *slots_out = slots;
+  *ksplit_out = ksplit;
+  *groups_out = groups;
+  return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -213,9 +279,13 @@ int svq_gemv(const void* x, const uint8_t* q, const uint16_t* s,
   a.n = n;
   a.k = k;
   a.y_f32 = y_dtype == SVQ_F32;
-  int lg = 0, rows = 0, wpg = 0, waves = 0, groups = 0;
+  int lg = 0, rows = 0, wpg = 0, waves = 0, groups = 0, slots = 0, ksplit = 0;
   hipError_t e;
-  if (choose_stream(m, n, k, qtype, tu, &lg, &rows, &wpg, &waves, &groups)) {
+  if (choose_mfma(m, n, k, qtype, tu, s, &rows, &slots, &ksplit, &groups)) {
+    a.slots = slots;
+    a.ksplit = ksplit;
+    e = svq::launch_gemv_mfma(a, qtype, m, rows, groups, static_cast<hipStream_t>(stream));
+  } else if (choose_stream(m, n, k, qtype, tu, &lg, &rows, &wpg, &waves, &groups)) {
     a.lg_g = lg;
     a.waves = waves;
     e = svq::launch_gemv_stream(a, qtype, m, rows, wpg, groups,
@@ -238,7 +308,12 @@ int svq_gemv_plan(int m, int n, int k, int qtype, int32_t* plan) {
   const Tuning tu = tuning();
   int lg = 0, rows = 0, wpg = 0, waves = 0, groups = 0, wmax = 0;
   for (int i = 0; i < 8; ++i) plan[i] = 0;
-  if (choose_stream(m, n, k, qtype, tu, &lg, &rows, &wpg, &waves, &groups, &wmax)) {
+  int slots = 0, ksplit = 0;
+  if (choose_mfma(m, n, k, qtype, tu, nullptr, &rows, &slots, &ksplit, &groups)) {
+    const int32_t p[8] = {3, ksplit, rows, slots * ksplit, groups * slots * ksplit, groups, slots,
+                          0};
+    for (int i = 0; i < 8; ++i) plan[i] = p[i];
+  } else if (choose_stream(m, n, k, qtype, tu, &lg, &rows, &wpg, &waves, &groups, &wmax)) {
     const int32_t p[8] = {1, lg, rows, wpg, waves, groups, wmax, 0};
     for (int i = 0; i < 8; ++i) plan[i] = p[i];
   } else {

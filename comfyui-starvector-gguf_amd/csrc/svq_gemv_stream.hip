@@ -31,6 +31,14 @@ namespace {
 
 constexpr uint32_t kOutOfRange = 0x80000000u;  // past every buffer range (< 2^31 bytes)
 
+// x pieces (16 bytes) per thread loaded before the weight prologue: at
+// M <= 2, all of x for K = 4608 with 256 threads; at larger M the batch of 4
+// that keeps the register peak of the staging below that of the main loop.
+template <int QT, int M>
+constexpr int kStageBatch =
+    M <= 2 ? M * 144 * (QTraits<QT>::kUnitWeights / 8) * QTraits<QT>::kUnitsPerBlock / 256 + 1
+           : 4;
+
 template <int QT, int M, int R, int D, int WPG>
 __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   using T = QTraits<QT>;
@@ -109,15 +117,19 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
     }
   };
 
-  // Stage x completely before the first weight load. Vector loads are served
-  // in issue order, so x loads issued behind the weight prologue would wait
-  // for the whole chip-wide prologue burst (tens of MB) and hold back the
-  // first compute; staged first, they cost one cache round trip.
-  stage_x<QT, M, WPG * 64>(a.x, k, 0, units, units, xs, sxs);
+  // The x loads go out first, then the weight prologue, and only then are the
+  // x registers written to LDS. Vector loads retire in issue order, so waiting
+  // for x does not wait for the weights, while the weight stream starts one
+  // cache round trip earlier than if x were staged completely first. (x loads
+  // issued behind the prologue would wait for the whole chip-wide prologue
+  // burst.) Pieces beyond the first batch are staged after the prologue.
+  XStager<QT, M, WPG * 64, kStageBatch<QT, M>> st(a.x, k, 0, units, units);
+  st.begin();
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d);
   uint32_t bias_bits[R];
   load_bias(wid, bias_bits);
+  st.finish(xs, sxs);
 
   float acc[R][M];
 #pragma unroll

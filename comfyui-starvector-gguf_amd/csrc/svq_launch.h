@@ -17,6 +17,8 @@ struct GemvArgs {
   int chunk_units;  // units of x staged in LDS at a time (chunked kernel)
   int y_f32;
   int waves;        // streaming waves in the grid (streaming kernel)
+  int slots;        // row tiles per workgroup (MFMA kernel)
+  int ksplit;       // K splits per row tile (MFMA kernel)
 };
 
 struct GemvShape {
@@ -41,6 +43,14 @@ size_t stream_lds_bytes(int qtype, int m, int k);
 const void* stream_kernel(int qtype, int m, int rows, int wpg);
 hipError_t launch_gemv_stream(const GemvArgs& a, int qtype, int m, int rows, int wpg,
                               int groups, hipStream_t stream);
+
+// MFMA kernel (svq_gemv_mfma.hip): blocks per step, LDS bytes, function
+// pointer (for occupancy queries) and launcher.
+int mfma_blocks_per_step(int qtype);
+size_t mfma_lds_bytes(int qtype, int m, int k, int rows, int wpg, int ksplit);
+const void* mfma_kernel(int qtype, int m, int rows);
+hipError_t launch_gemv_mfma(const GemvArgs& a, int qtype, int m, int rows, int groups,
+                            hipStream_t stream);
 
 hipError_t launch_dequant(const uint8_t* q, const uint16_t* s, void* out,
                           int64_t nblocks, int qtype, int out_dtype,

@@ -201,9 +201,12 @@ def decoder_cases():
     return cases
 
 
+@pytest.mark.parametrize("kernel_path", ["auto", "mfma"], indirect=True)
 @pytest.mark.parametrize("qtype,n,k,m,has_bias", decoder_cases())
-def test_gemv_decoder_shapes(cuda_device, qtype, n, k, m, has_bias):
-    say(f"gemv decoder shape {qtype} m={m} n={n} k={k} bias={has_bias}")
+def test_gemv_decoder_shapes(cuda_device, kernel_path, qtype, n, k, m, has_bias):
+    say(f"gemv decoder shape {kernel_path} {qtype} m={m} n={n} k={k} bias={has_bias}")
+    if kernel_path == "mfma":
+        assert native.gemv_plan(m, n, k, qtype)["kernel"] == "mfma"
     q, s = gpu_soa(qtype, n, k, seed=n + k + m, dev=cuda_device)
     g = torch.Generator(device=cuda_device).manual_seed(m)
     x = torch.randn((m, k), generator=g, device=cuda_device).half()
@@ -256,18 +259,29 @@ def test_gemv_fp16_denormal_activations(cuda_device):
 
 @pytest.fixture
 def kernel_path(request, monkeypatch):
-    """Force the streaming or the chunked GEMV kernel (read per call)."""
+    """Force the MFMA, streaming or chunked GEMV kernel (read per call)."""
     monkeypatch.setenv("SVQ_PATH", request.param)
     return request.param
 
 
-@pytest.mark.parametrize("kernel_path", ["stream", "chunked"], indirect=True)
+def mfma_eligible(qtype, m, n, k):
+    """Shapes the MFMA kernel takes: whole steps of K, x in LDS."""
+    kb = k // 32
+    bps = 2 if qtype == "Q8_0" else 4
+    lds = kb * 4 * m * 16 + kb * (m + 3) // 4 * 4 * 4
+    return kb % bps == 0 and lds <= 156 * 1024
+
+
+@pytest.mark.parametrize("kernel_path", ["mfma", "stream", "chunked"], indirect=True)
 @pytest.mark.parametrize("qtype", QTYPES)
-def test_gemv_both_kernels_against_oracle(cuda_device, kernel_path, qtype):
+def test_gemv_every_kernel_against_oracle(cuda_device, kernel_path, qtype):
     rng = np.random.default_rng(7)
     for m in (1, 2, 3, 8):
         for n, k in ((1, 32), (13, 128), (33, 192), (129, 2048), (515, 4608), (40, 18432)):
             say(f"gemv {kernel_path} {qtype} m={m} n={n} k={k}")
+            if kernel_path == "mfma":
+                plan = native.gemv_plan(m, n, k, qtype)
+                assert (plan["kernel"] == "mfma") == mfma_eligible(qtype, m, n, k), plan
             q, s = orc.synthetic_soa(qtype, n, k, seed=n + k + m)
             x = rng.standard_normal((m, k)).astype(np.float16)
             bias = rng.standard_normal(n).astype(np.float16)
@@ -295,3 +309,34 @@ def test_gemv_every_launch_shape(cuda_device, monkeypatch, lg_g, rows):
                 y = hip_gemv(to_dev(x, cuda_device), to_dev(q, cuda_device), to_dev(s, cuda_device), qtype,
                              n, None, torch.float32)
                 assert orc.rel_err(y.cpu().numpy(), ref) <= FP32_TOL, (lg_g, rows, path, qtype, m, n, k)
+
+
+@pytest.mark.parametrize("rows", (1, 2))
+@pytest.mark.parametrize("ksplit", (1, 2, 3, 5, 8, 16))
+def test_gemv_every_mfma_launch_shape(cuda_device, monkeypatch, rows, ksplit):
+    """Every MFMA tile / K-split / tile-slot choice, on ragged row counts."""
+    monkeypatch.setenv("SVQ_PATH", "mfma")
+    monkeypatch.setenv("SVQ_MFMA_R", str(rows))
+    monkeypatch.setenv("SVQ_MFMA_S", str(ksplit))
+    rng = np.random.default_rng(rows * 100 + ksplit)
+    for slots in (1, 2, 4):
+        if slots * ksplit > 16:
+            continue
+        monkeypatch.setenv("SVQ_MFMA_P", str(slots))
+        for qtype in QTYPES:
+            for m, n, k in ((1, 77, 2048), (2, 130, 1152), (5, 35, 512), (8, 200, 4608)):
+                say(f"gemv mfma rows={rows} ksplit={ksplit} slots={slots} {qtype} m={m} n={n} k={k}")
+                plan = native.gemv_plan(m, n, k, qtype)
+                steps = k // 32 // (2 if qtype == "Q8_0" else 4)
+                assert plan["kernel"] == "mfma", plan
+                assert plan["lg_g"] == min(ksplit, steps), plan  # K splits in use
+                q, s = orc.synthetic_soa(qtype, n, k, seed=m * n + k)
+                x = rng.standard_normal((m, k)).astype(np.float16)
+                bias = rng.standard_normal(n).astype(np.float16)
+                ref = orc.gemv_ref(x, q, s, qtype, n, k, bias)
+                y = hip_gemv(to_dev(x, cuda_device), to_dev(q, cuda_device), to_dev(s, cuda_device),
+                             qtype, n, to_dev(bias, cuda_device), torch.float32)
+                assert orc.rel_err(y.cpu().numpy(), ref) <= FP32_TOL, (rows, ksplit, slots, qtype, m, n, k)
+                y16 = hip_gemv(to_dev(x, cuda_device), to_dev(q, cuda_device), to_dev(s, cuda_device),
+                               qtype, n, to_dev(bias, cuda_device), torch.float16)
+                assert orc.rel_err(y16.float().cpu().numpy(), ref) <= FP16_TOL
