@@ -366,6 +366,115 @@ def cpu_baseline(seconds_budget=20.0):
             "ms_per_step": round(elapsed * 1e3, 1), "per_shape": per}
 
 
+# StarCoder2-8B-style decode loop: 32 layers, Q4_0 weights, beam 2, a
+# 1024-token prefill whose first 576 vectors are the seeded vision prompt,
+# then a fixed number of decode steps (random end-of-sequence tokens cannot
+# stop it).
+DECODE = {"qtype": "Q4_0", "beams": 2, "prompt": 576, "prefill": 1024, "steps": 512}
+
+
+def decode_model(dev):
+    from starvector_amd.decoder import DecoderConfig, Starcoder2Decoder
+    cfg = DecoderConfig()
+    return cfg, Starcoder2Decoder(cfg, qtype=DECODE["qtype"], seed=0, device=dev)
+
+
+def decode_prompt(cfg, dev, length, dtype=torch.float16):
+    """The seeded vision prompt (576 fp16 N(0,1) vectors), extended with
+    further seeded vectors to `length` prefill tokens."""
+    g = torch.Generator(device=dev).manual_seed(1)
+    vision = torch.randn((1, min(length, DECODE["prompt"]), cfg.hidden), generator=g, device=dev)
+    extra = torch.randn((1, max(0, length - DECODE["prompt"]), cfg.hidden), generator=g, device=dev)
+    return torch.cat((vision, extra), 1).to(dtype)
+
+
+def run_decode(model, emb, steps, sync):
+    """Beam-2 decode of `steps` steps; returns wall-clock marks (seconds)."""
+    from starvector_amd.decoder import beam_steps
+    marks = {}
+
+    def mark(key):
+        sync()
+        marks[key] = time.perf_counter()
+
+    torch.manual_seed(0)
+    with torch.inference_mode():
+        mark("start")
+        beam_steps(model, emb, steps, DECODE["beams"], on_prefill=lambda: mark("prefill"),
+                   on_step=lambda i: mark("first") if i == 1 else None)
+        mark("end")
+    return marks
+
+
+def decode_bench(dev, steps):
+    """Decode rate of the 8B-style loop on the GPU (every quantized linear on
+    the HIP GEMV; attention, norms and sampling in torch)."""
+    cfg, model = decode_model(dev)
+    sync = torch.cuda.synchronize
+    run_decode(model, decode_prompt(cfg, dev, 64), 3, sync)  # loads kernels and GEMM libraries
+    marks = run_decode(model, decode_prompt(cfg, dev, DECODE["prefill"]), steps, sync)
+    decode_s = marks["end"] - marks["first"]
+    result = {
+        "workload": f"StarCoder2-8B-style decoder, {cfg.layers} layers, hidden {cfg.hidden}, "
+                    f"{cfg.heads}/{cfg.kv_heads} heads, inner {cfg.inner}, vocab {cfg.vocab}, "
+                    f"{DECODE['qtype']} weights (seeded synthetic), beam {DECODE['beams']}, prefill "
+                    f"{DECODE['prefill']} tokens (576-vector vision prompt), {steps} decode steps",
+        "steps": steps,
+        "decode_steps_per_s": round((steps - 1) / decode_s, 2),
+        "decode_ms_per_step": round(decode_s / (steps - 1) * 1e3, 3),
+        "tokens_per_s_incl_prefill": round(steps / (marks["end"] - marks["start"]), 2),
+        "prefill_ms": round((marks["prefill"] - marks["start"]) * 1e3, 1),
+        "first_step_ms": round((marks["first"] - marks["prefill"]) * 1e3, 1),
+        "weight_bytes_per_step": decoder_weight_bytes(cfg),
+    }
+    return result, model, cfg
+
+
+def decoder_weight_bytes(cfg):
+    per_layer = [(cfg.hidden + 2 * cfg.kv_heads * cfg.head_dim, cfg.hidden), (cfg.hidden, cfg.hidden),
+                 (cfg.inner, cfg.hidden), (cfg.hidden, cfg.inner)]
+    bb = BLOCK_BYTES[DECODE["qtype"]]
+    return cfg.layers * sum(n * k // 32 * bb for n, k in per_layer) + cfg.vocab * cfg.hidden // 32 * bb
+
+
+def decode_cpu_baseline(model, cfg, steps=2, prompt=16):
+    """The same decoder on the host cores through the reference's CPU path
+    (fp32; every quantized linear as tiled dequantize + F.linear), for a
+    short prompt and a few decode steps."""
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    model.to_host()
+    emb = decode_prompt(cfg, torch.device("cpu"), prompt, torch.float32)
+    marks = run_decode(model, emb, steps, lambda: None)
+    per_step = (marks["end"] - marks["prefill"]) / steps
+    return {"decode_steps_per_s": round(1 / per_step, 4), "decode_ms_per_step": round(per_step * 1e3, 1),
+            "cores": threads, "kind": "port",
+            "sample": f"{steps} beam-2 decode steps after a {prompt}-token prefill, same 32-layer "
+                      f"model on the host in fp32 (reference CPU path per quantized linear)"}
+
+
+def summarize_decode(trace: Path):
+    """GEMV share of the decode steps in a kernel trace of `--decode-only`:
+    dispatches after the last dequantize kernel of the measured prefill."""
+    rows = sorted(_read_csv(trace), key=lambda r: int(r["Dispatch_Id"]))
+    last = max(i for i, r in enumerate(rows) if "dequant_kernel" in r["Kernel_Name"])
+    phase = rows[last + 1:]
+    durs = _durations_us(phase)
+    total = sum(durs)
+    gemv = sum(d for d, r in zip(durs, phase) if _is_gemv(r["Kernel_Name"]))
+    by = {}
+    for d, r in zip(durs, phase):
+        key = _short_kernel(r["Kernel_Name"])[:70]
+        by[key] = by.get(key, 0.0) + d
+    span = (int(phase[-1]["End_Timestamp"]) - int(phase[0]["Start_Timestamp"])) / 1e3
+    out = [f"decode phase: {len(phase)} dispatches, kernel time {total:.0f} us, span {span:.0f} us",
+           f"GEMV kernels: {gemv:.0f} us = {gemv / total:.1%} of kernel time, {gemv / span:.1%} of the span",
+           "| kernel | total us | share |", "|---|---|---|"]
+    for key, d in sorted(by.items(), key=lambda kv: -kv[1])[:15]:
+        out.append(f"| {key} | {d:.0f} | {d / total:.1%} |")
+    print("\n".join(out))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -376,6 +485,12 @@ def main():
     ap.add_argument("--summarize", metavar="DIR",
                     help="summarize rocprofv3 CSV output of --profile runs under DIR (kernel "
                          "trace and counter collections) per step GEMV shape, then exit")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode-loop measurement")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the decode loop (for kernel traces) and print its JSON")
+    ap.add_argument("--decode-steps", type=int, default=DECODE["steps"])
+    ap.add_argument("--summarize-decode", metavar="CSV",
+                    help="GEMV share of the decode steps in a kernel trace of --decode-only, then exit")
     ap.add_argument("--profile", action="store_true",
                     help="eager launches for rocprofv3: every step GEMV on 8 copies, twice, then "
                          "16 torch copies of 256 MiB (the known-size copy that scales FETCH_SIZE "
@@ -383,6 +498,9 @@ def main():
     args = ap.parse_args()
     if args.summarize:
         summarize(Path(args.summarize))
+        return
+    if args.summarize_decode:
+        summarize_decode(Path(args.summarize_decode))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -396,6 +514,10 @@ def main():
     log(f"device: {torch.cuda.get_device_name(dev)}")
     if args.profile:
         profile_pass(dev, stream)
+        return
+    if args.decode_only:
+        result, _, _ = decode_bench(dev, args.decode_steps)
+        print(json.dumps(result), flush=True)
         return
 
     # --- headline step: 8 passes over the 5 matrices, distinct copies -------
@@ -457,6 +579,16 @@ def main():
         cpu = cpu_baseline()
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
 
+    decode = None
+    if not args.quick and not args.no_decode:
+        decode, model, cfg = decode_bench(dev, args.decode_steps)
+        log(f"decode: {decode['decode_steps_per_s']} steps/s ({decode['decode_ms_per_step']} ms/step), "
+            f"{decode['tokens_per_s_incl_prefill']} tokens/s incl. prefill")
+        if not args.no_cpu:
+            decode["cpu_baseline"] = decode_cpu_baseline(model, cfg)
+            log(f"decode cpu baseline: {decode['cpu_baseline']['decode_ms_per_step']} ms/step")
+        del model
+
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": steps, "warmup": warm_replays * COPIES, "ms_per_step": round(ms_step, 5),
@@ -469,6 +601,7 @@ def main():
                    "frac_of_peak": round(value / PEAK_HBM_GBS, 4), "weight_copies": COPIES},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "decode": decode,
         "sweep": sweep,
     }
     print(json.dumps(result), flush=True)

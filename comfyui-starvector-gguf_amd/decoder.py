@@ -179,6 +179,16 @@ class Starcoder2Decoder(nn.Module):
     def embed(self, ids):
         return self.embed_tokens(ids)
 
+    def to_host(self):
+        """Move to the CPU in fp32, the dtype the reference's loader uses on a
+        CPU (its GGUFLinear then runs the tiled dequantize + F.linear path)."""
+        self.to("cpu")
+        for module in self.modules():
+            if isinstance(module, nn.LayerNorm):
+                module.float()
+        self.embed_tokens.output_dtype = torch.float32
+        return self
+
     def prefill(self, embeddings, rows, capacity):
         """Encode the prompt once (batch 1); its cache serves all `rows`."""
         cfg = self.cfg
@@ -274,11 +284,12 @@ def warp(scores, temperature, top_p, keep):
 
 
 def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, capacity=None,
-               on_prefill=None):
+               on_prefill=None, on_step=None):
     """Beam sampling (runtime_shared.py:214-265) for a fixed number of decode
     steps: every step samples 2 * beams continuations from all beams, keeps
     the best `beams`, reorders the cache and decodes. End-of-sequence tokens
     do not stop it, so every call performs exactly `steps` decode steps.
+    `on_prefill()` runs after the prefill and `on_step(i)` after decode step i.
     Returns (best token sequence, per-step running scores)."""
     keep = 2 * beams
     capacity = capacity or embeddings.shape[1] + steps + 1
@@ -306,4 +317,6 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
         seen[torch.arange(beams, device=device), next_tokens] = True
         decoding.reorder([parents[j] for j in order])
         logits = decoding.step(next_tokens)
+        if on_step is not None:
+            on_step(step + 1)
     return running[0], running_scores

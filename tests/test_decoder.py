@@ -1,0 +1,115 @@
+"""The StarCoder2-style decode harness (the reference's runtime_8b.py
+Starcoder2Block / Starcoder2 and runtime_shared.py CachedDecoding /
+_beam_sample) on a small configuration.
+
+Teacher forcing pins the cache machinery: decoding token t after a prefill
+of L positions must give the logits that a prefill of the L + 1 positions
+gives at its last position (same RoPE angles, same keys and values, same
+mask). On the GPU, the decoder whose linears run the HIP GEMV is compared
+with the same decoder whose linears dequantize and call F.linear, and graph
+replays with eager decode steps.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import starvector_amd.quantization as quantization
+from starvector_amd.decoder import DecoderConfig, Starcoder2Decoder, beam_steps
+
+SMALL = DecoderConfig(hidden=256, heads=4, kv_heads=2, inner=512, layers=2, vocab=320,
+                      window=4096, context=512)
+
+
+def small_model(device, qtype="Q4_0"):
+    model = Starcoder2Decoder(SMALL, qtype=qtype, seed=3, device=device)
+    return model.to_host() if device == "cpu" else model
+
+
+def prompt(length, device, dtype):
+    g = torch.Generator(device=device).manual_seed(7)
+    return torch.randn((1, length, SMALL.hidden), generator=g, device=device).to(dtype)
+
+
+def teacher_forced(model, emb, token):
+    """(decode-step logits, prefill logits) for `token` after `emb`."""
+    with torch.inference_mode():
+        decoding, _ = model.prefill(emb, 2, emb.shape[1] + 4)
+        stepped = decoding.step(torch.tensor([token, token], device=emb.device)).clone()
+        extended = torch.cat((emb, model.embed(torch.tensor([[token]], device=emb.device)).to(emb.dtype)), 1)
+        _, full = model.prefill(extended, 1, extended.shape[1] + 1)
+    return stepped, full
+
+
+@pytest.mark.parametrize("qtype", ("Q4_0", "Q5_0", "Q8_0"))
+def test_decode_step_matches_prefill_cpu(qtype):
+    model = small_model("cpu", qtype)
+    stepped, full = teacher_forced(model, prompt(9, "cpu", torch.float32), 17)
+    assert torch.equal(stepped[0], stepped[1])
+    err = ((stepped[0] - full[0]).abs().max() / full.abs().max()).item()
+    assert err <= 1e-4, err
+
+
+def test_beam_steps_cpu():
+    model = small_model("cpu")
+    torch.manual_seed(0)
+    with torch.inference_mode():
+        tokens, scores = beam_steps(model, prompt(5, "cpu", torch.float32), 4, beams=2)
+    assert len(tokens) == 4 and all(0 <= t < SMALL.vocab for t in tokens)
+    assert len(scores) == 2
+
+
+@pytest.mark.gpu
+def test_decode_step_matches_prefill_gpu(cuda_device):
+    model = small_model(cuda_device)
+    stepped, full = teacher_forced(model, prompt(9, cuda_device, torch.float16), 17)
+    err = ((stepped[0].float() - full[0].float()).abs().max() / full.float().abs().max()).item()
+    assert err <= 2e-2, err
+
+
+@pytest.mark.gpu
+def test_decoder_hip_gemv_matches_torch_linears(cuda_device, monkeypatch):
+    """Same decoder, same teacher-forced tokens: HIP GEMV linears versus
+    dequantize + F.linear linears (the fallback path) on the GPU."""
+    model = small_model(cuda_device)
+    emb = prompt(12, cuda_device, torch.float16)
+    tokens = [5, 300, 17, 17]
+
+    def run():
+        out = []
+        with torch.inference_mode():
+            decoding, logits = model.prefill(emb, 2, 32)
+            out.append(logits.float().clone())
+            for t in tokens:
+                out.append(decoding.step(torch.tensor([t, t + 1], device=cuda_device)).float().clone())
+        return torch.stack(out)
+
+    hip = run()
+    monkeypatch.setattr(quantization, "_fused_soa_linear", lambda *a, **k: None)
+    ref = run()
+    err = ((hip - ref).abs().max() / ref.abs().max()).item()
+    assert err <= 2e-2, err
+
+
+@pytest.mark.gpu
+def test_graph_replays_match_eager_decode(cuda_device):
+    """CachedDecoding replays one captured graph per span; every replay, with
+    eager work and synchronization between replays, matches an eager decode of
+    the same step."""
+    model = small_model(cuda_device)
+    emb = prompt(12, cuda_device, torch.float16)
+    tokens = [(5, 6), (300, 2), (17, 17), (1, 319)]
+    with torch.inference_mode():
+        decoding, _ = model.prefill(emb, 2, 40)
+        eager, _ = model.prefill(emb, 2, 40)
+        for a, b in tokens:
+            t = torch.tensor([a, b], device=cuda_device)
+            got = decoding.step(t).float().clone()
+            torch.cuda.synchronize()
+            eager.tokens.copy_(t)
+            want = eager._decode(decoding.span()).float()
+            eager.position += 1
+            eager.length += 1
+            assert len(decoding.graphs) == 1
+            err = ((got - want).abs().max() / want.abs().max()).item()
+            assert err <= 1e-3, err
