@@ -159,13 +159,17 @@ bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out
   const int wpg = svq::kStreamWavesPerGroup;
   const int units = (k / 32) * svq::units_per_block(qtype);
   const int lg0 = base_lg_g(units);
+  // Widening a row group below 4 units per lane costs more in per-wave
+  // overhead (staging, reduction, idle lanes) than the extra waves recover.
+  int lg_cap = lg0;
+  while (lg_cap < 6 && (units >> (lg_cap + 1)) >= 4) ++lg_cap;
   int lg = lg0, rows = 2, wmax = 0, tiles = 0;
   for (;;) {
     wmax = cus * waves_per_cu(dev, svq::stream_kernel(qtype, m, rows, wpg), wpg, lds);
     tiles = (n + ((64 >> lg) * rows) - 1) / ((64 >> lg) * rows);
     if (tiles >= wmax) break;
     if (rows == 2) rows = 1;
-    else if (lg < 6) ++lg;
+    else if (lg < lg_cap) ++lg;
     else break;
   }
   if (tu.lg_g >= 0) lg = tu.lg_g;

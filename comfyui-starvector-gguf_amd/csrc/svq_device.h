@@ -131,6 +131,46 @@ __device__ __forceinline__ void unpack<5>(const uint32_t (&w)[5],
   }
 }
 
+// Q5_0 mask expansion through a 256-entry LDS table: entry b (8 bytes at
+// byte offset 8 * b) holds {spread4(b & 15), spread4(b >> 4)}, the fifth bits
+// of 8 consecutive weights as bytes. The table sits at LDS offset 0, so a
+// lookup address is 8 * (mask byte): two instructions per 8 weights instead
+// of six for the multiply-and-mask spread.
+constexpr int kQ5TableBytes = 256 * 8;
+
+__device__ __forceinline__ void build_q5_table(u32x2* table, int tid, int nthreads) {
+  for (int b = tid; b < 256; b += nthreads) {
+    u32x2 e;
+    e.x = spread4((uint32_t)b & 15u);
+    e.y = spread4((uint32_t)b >> 4);
+    table[b] = e;
+  }
+}
+
+// unpack<5> with the mask bits expanded by table lookups (same output).
+__device__ __forceinline__ void unpack_q5_table(const uint32_t (&w)[5], uint32_t (&p)[16],
+                                                const u32x2* table) {
+  const uint32_t qh = w[0];
+  const char* base = reinterpret_cast<const char*>(table);
+  // Mask byte k, times 8 (the table stride), as a byte offset.
+  const u32x2 b0 = *reinterpret_cast<const u32x2*>(base + 8u * (qh & 0xffu));
+  const u32x2 b1 = *reinterpret_cast<const u32x2*>(base + 8u * ((qh >> 8) & 0xffu));
+  const u32x2 b2 = *reinterpret_cast<const u32x2*>(base + 8u * ((qh >> 16) & 0xffu));
+  const u32x2 b3 = *reinterpret_cast<const u32x2*>(base + 8u * (qh >> 24));
+  const uint32_t blo[4] = {b0.x, b0.y, b1.x, b1.y};  // weights 0-15
+  const uint32_t bhi[4] = {b2.x, b2.y, b3.x, b3.y};  // weights 16-31
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t v = w[1 + i];
+    const uint32_t lo = (v << 4) & 0xf0f0f0f0u;
+    const uint32_t hi = v & 0xf0f0f0f0u;
+    p[2 * i] = perm(blo[i], lo, kSelB01H);
+    p[2 * i + 1] = perm(blo[i], lo, kSelB23H);
+    p[8 + 2 * i] = perm(bhi[i], hi, kSelB01H);
+    p[8 + 2 * i + 1] = perm(bhi[i], hi, kSelB23H);
+  }
+}
+
 template <>
 __device__ __forceinline__ void unpack<8>(const uint32_t (&w)[4],
                                           uint32_t (&p)[8]) {

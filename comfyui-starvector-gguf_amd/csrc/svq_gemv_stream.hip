@@ -70,8 +70,12 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)n * (uint32_t)kb * 2u);
   const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bias, a.bias ? (uint32_t)n * 2u : 0u);
 
+  // Static LDS: the Q5_0 mask table (a compile-time address, so lookups
+  // need no base register). Dynamic LDS: x pieces, then offset sums.
+  __shared__ u32x2 q5_table[QT == 5 ? 256 : 1];
+  if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
   u32x4* xs = lds;
-  float* sxs = reinterpret_cast<float*>(lds + M * P * units);
+  float* sxs = reinterpret_cast<float*>(xs + M * P * units);
 
   // Row byte offsets of this lane's R rows in tile `tile` (clamped to n - 1:
   // loaded, never stored).
@@ -146,7 +150,10 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
         if (u < units) {
           uint32_t pk[R][XW];
 #pragma unroll
-          for (int r = 0; r < R; ++r) unpack<QT>(w[d][r], pk[r]);
+          for (int r = 0; r < R; ++r) {
+            if constexpr (QT == 5) unpack_q5_table(w[d][r], pk[r], q5_table);
+            else unpack<QT>(w[d][r], pk[r]);
+          }
           float dsc[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) dsc[r] = half_bits_to_float((uint16_t)sc[d][r]);
