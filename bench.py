@@ -52,6 +52,10 @@ STEP_SHAPES = [  # (name, n, k, has_bias) of the 8B decoder step, Q5_0, batch 2
 STEP_QTYPE, STEP_M, COPIES = "Q5_0", 2, 8
 
 
+KERNEL_NAMES = {"stream": "svq::gemv_stream_kernel", "chunked": "svq::gemv_kernel",
+                "mfma": "svq::gemv_mfma_kernel", "mfma4": "svq::gemv_mfma4_kernel"}
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -552,6 +556,7 @@ def main():
 
     # --- dominant launch: lm_head, own graph over its 8 copies -------------
     hname, hn, hk, hbias = STEP_SHAPES[-1]
+    head_plan = native.gemv_plan(STEP_M, hn, hk, STEP_QTYPE)
     hgraph = capture(per_shape[hname], stream)
     time_graph(hgraph, stream, 2)
     head_ms = statistics.median(time_graph(hgraph, stream, 5) / COPIES for _ in range(5))
@@ -561,7 +566,8 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": committed_traffic(hname, hn, hk),
                 "traffic_source": TRAFFIC_SUMMARY.name,
-                "kernel": f"svq gemv_stream_kernel {STEP_QTYPE} M={STEP_M} lm_head {hn}x{hk}",
+                "kernel": f"{KERNEL_NAMES[head_plan['kernel']]} {STEP_QTYPE} M={STEP_M} lm_head {hn}x{hk}",
+                "launch": head_plan,
                 "us_per_launch": round(head_ms * 1e3, 2), "bytes_per_launch": head_bytes}
     log(f"lm_head: {head_ms * 1e3:.2f} us, {achieved:.1f} GB/s")
 

@@ -115,7 +115,7 @@ def gemv_plan(m: int, n: int, k: int, qtype: str) -> dict:
     out = (ctypes.c_int32 * 8)()
     _check(lib, "svq_gemv_plan", lib.svq_gemv_plan(m, n, k, QTYPE_CODE[qtype], out))
     plan = dict(zip(PLAN_FIELDS, list(out)))
-    plan["kernel"] = {1: "stream", 2: "chunked", 3: "mfma"}[plan["kernel"]]
+    plan["kernel"] = {1: "stream", 2: "chunked", 3: "mfma", 4: "mfma4"}[plan["kernel"]]
     return plan
 
 

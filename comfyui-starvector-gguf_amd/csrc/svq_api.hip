@@ -43,16 +43,17 @@ bool aligned(const void* p, uintptr_t a) {
 }
 
 // Launch-shape overrides for tuning sweeps and for tests that exercise every
-// kernel: SVQ_PATH ("mfma", "stream" or "chunked"), SVQ_LG_G (log2 lanes per
+// kernel: SVQ_PATH ("mfma4", "mfma", "stream" or "chunked"), SVQ_LG_G (log2 lanes per
 // row, 0..6) and SVQ_ROWS (rows per lane group, 1 or 2) of the streaming and
 // chunked kernels, SVQ_LDS_KB (LDS budget of the chunked kernel), and
-// SVQ_MFMA_R (16-row tiles per wave, 1 or 2), SVQ_MFMA_S (K splits, 1..16) and
+// SVQ_MFMA_R (MFMA row tiles per wave, 1 or 2; for the streaming MFMA kernel
+// 3 selects its three-units-per-lane Q5_0 variant), SVQ_MFMA_S (K splits, 1..16) and
 // SVQ_MFMA_P (tile slots per workgroup) of the MFMA kernel. Read on every
 // call, so a process may change them.
 struct Tuning {
   int lg_g = -1;
   int rows = 0;
-  int path = 0;  // 0 automatic, 1 streaming, 2 chunked, 3 mfma
+  int path = 0;  // 0 automatic, 1 streaming, 2 chunked, 3 mfma, 4 streaming mfma
   int lds_kb = 40;
   int mfma_r = 0, mfma_s = 0, mfma_p = 0;
 };
@@ -65,6 +66,7 @@ Tuning tuning() {
     t.path = strcmp(v, "stream") == 0    ? 1
              : strcmp(v, "chunked") == 0 ? 2
              : strcmp(v, "mfma") == 0    ? 3
+             : strcmp(v, "mfma4") == 0   ? 4
                                          : 0;
   if (const char* v = getenv("SVQ_LDS_KB")) t.lds_kb = atoi(v);
   if (const char* v = getenv("SVQ_MFMA_R")) t.mfma_r = atoi(v);
@@ -73,7 +75,7 @@ Tuning tuning() {
   if (t.lg_g > 6) t.lg_g = 6;
   if (t.rows != 0 && t.rows != 1 && t.rows != 2) t.rows = 0;
   if (t.lds_kb < 4 || t.lds_kb > 64) t.lds_kb = 40;
-  if (t.mfma_r != 1 && t.mfma_r != 2) t.mfma_r = 0;
+  if (t.mfma_r < 1 || t.mfma_r > 3) t.mfma_r = 0;
   if (t.mfma_s < 0 || t.mfma_s > 16) t.mfma_s = 0;
   if (t.mfma_p < 0 || t.mfma_p > 16) t.mfma_p = 0;
   return t;
@@ -199,9 +201,55 @@ constexpr int kMfmaMinRows = 5;  // smallest M sent to the MFMA kernel by defaul
 // when the shape or alignment does not suit the kernel: K must be a whole
 // number of steps (4 blocks, 2 for Q8_0), the scales 4-byte aligned, x and
 // its offset sums must fit in LDS, and the arrays below 2^31 bytes.
+// Streaming MFMA launch (M <= 4): row tiles of 4 * R rows over 16 unit
+// slots; two row sets per lane first (each x read serves both), one when that
+// leaves fewer tiles than resident waves; persistent waves trimmed to equal
+// tile counts, as for the vector streaming kernel.
+bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_out,
+                  int* waves_out, int* groups_out, int* wmax_out) {
+  if ((tu.path != 4 && tu.path != 0) || m > 4) return false;
+  // Automatic choice (measured at the StarCoder2-8B and GPTBigCode-1B shapes):
+  // the matrix-core path wins for Q5_0 at every M and for Q4_0 / Q8_0 from
+  // M = 2; at M = 1 the vector path's dot products are cheap enough.
+  if (tu.path == 0 && qtype != SVQ_Q5_0 && m < 2) return false;
+  const size_t lds = svq::stream_lds_bytes(qtype, m, k);
+  const uint64_t q_bytes = (uint64_t)n * (k / 32) * payload_bytes(qtype);
+  if (lds > kStreamLdsMax || q_bytes >= (1ull << 31) || (uint64_t)n * (k / 16) >= (1ull << 31))
+    return false;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const int cus = device_cus(dev);
+  const int wpg = svq::kStreamWavesPerGroup;
+  // Variants (the `rows` code): 3 = Q5_0 with three consecutive units per
+  // lane (needs units % 48 == 0), 2 = two row sets per lane, 1 = one.
+  const int units = (k / 32) * svq::units_per_block(qtype);
+  const bool triple = qtype == SVQ_Q5_0 && units % 48 == 0;
+  int rows = tu.mfma_r ? tu.mfma_r : (triple ? 3 : 2), wmax = 0, tiles = 0;
+  if (rows == 3 && !triple) rows = 2;
+  for (;;) {
+    wmax = cus * waves_per_cu(dev, svq::mfma4_kernel(qtype, m, rows), wpg, lds);
+    const int tile_rows = rows == 2 ? 8 : 4;
+    tiles = (n + tile_rows - 1) / tile_rows;
+    if (tiles >= wmax || rows != 2 || tu.mfma_r) break;
+    rows = 1;
+  }
+  // Long rows with too few tiles to fill the GPU: 16 unit slots per row leave
+  // waves that are long and few; the vector kernel spreads a row over 64 lanes.
+  if (tu.path == 0 && k > 8192 && tiles < wmax) return false;
+  int waves = tiles < wmax ? tiles : wmax;
+  const int rounds = (tiles + waves - 1) / waves;
+  const int balanced = (tiles + rounds - 1) / rounds;
+  if (balanced >= wmax - wmax / 16) waves = balanced;
+  *rows_out = rows;
+  *waves_out = waves;
+  *groups_out = (waves + wpg - 1) / wpg;
+  *wmax_out = wmax;
+  return true;
+}
+
 bool choose_mfma(int m, int n, int k, int qtype, const Tuning& tu, const void* s, int* rows_out,
                  int* slots_out, int* ksplit_out, int* groups_out) {
-  if (tu.path == 1 || tu.path == 2) return false;
+  if (tu.path == 1 || tu.path == 2 || tu.path == 4) return false;
   // Automatic choice: the matrix cores pay off once the per-weight dot work
   // (M fp32 FMAs per weight on the vector path) outweighs the MFMA path's
   // fixed cost; measured crossover at MI355X decoder shapes is M = 4..5.
@@ -215,7 +263,7 @@ bool choose_mfma(int m, int n, int k, int qtype, const Tuning& tu, const void* s
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   const int cus = device_cus(dev);
-  const int rows = tu.mfma_r ? tu.mfma_r : (m >= kMfmaMinRows ? 2 : 1);
+  const int rows = tu.mfma_r == 1 || tu.mfma_r == 2 ? tu.mfma_r : (m >= kMfmaMinRows ? 2 : 1);
   const int tiles = (n + 16 * rows - 1) / (16 * rows);
   int ksplit = 1;
   if (tu.mfma_s) {
@@ -285,7 +333,11 @@ int svq_gemv(const void* x, const uint8_t* q, const uint16_t* s,
   a.y_f32 = y_dtype == SVQ_F32;
   int lg = 0, rows = 0, wpg = 0, waves = 0, groups = 0, slots = 0, ksplit = 0;
   hipError_t e;
-  if (choose_mfma(m, n, k, qtype, tu, s, &rows, &slots, &ksplit, &groups)) {
+  int wmax = 0;
+  if (choose_mfma4(m, n, k, qtype, tu, &rows, &waves, &groups, &wmax)) {
+    a.waves = waves;
+    e = svq::launch_gemv_mfma4(a, qtype, m, rows, groups, static_cast<hipStream_t>(stream));
+  } else if (choose_mfma(m, n, k, qtype, tu, s, &rows, &slots, &ksplit, &groups)) {
     a.slots = slots;
     a.ksplit = ksplit;
     e = svq::launch_gemv_mfma(a, qtype, m, rows, groups, static_cast<hipStream_t>(stream));
@@ -313,7 +365,10 @@ int svq_gemv_plan(int m, int n, int k, int qtype, int32_t* plan) {
   int lg = 0, rows = 0, wpg = 0, waves = 0, groups = 0, wmax = 0;
   for (int i = 0; i < 8; ++i) plan[i] = 0;
   int slots = 0, ksplit = 0;
-  if (choose_mfma(m, n, k, qtype, tu, nullptr, &rows, &slots, &ksplit, &groups)) {
+  if (choose_mfma4(m, n, k, qtype, tu, &rows, &waves, &groups, &wmax)) {
+    const int32_t p[8] = {4, 4, rows, svq::kStreamWavesPerGroup, waves, groups, wmax, 0};
+    for (int i = 0; i < 8; ++i) plan[i] = p[i];
+  } else if (choose_mfma(m, n, k, qtype, tu, nullptr, &rows, &slots, &ksplit, &groups)) {
     const int32_t p[8] = {3, ksplit, rows, slots * ksplit, groups * slots * ksplit, groups, slots,
                           0};
     for (int i = 0; i < 8; ++i) plan[i] = p[i];

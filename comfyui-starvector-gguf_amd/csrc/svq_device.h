@@ -112,6 +112,20 @@ __device__ __forceinline__ void unpack<4>(const uint32_t (&w)[4],
   }
 }
 
+// unpack<4> with both nibble halves as 16 * code, for dot products that sum
+// the two halves together (offset term and output scale as for Q5_0).
+__device__ __forceinline__ void unpack_q4_x16(const uint32_t (&w)[4], uint32_t (&p)[16]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = (w[i] << 4) & 0xf0f0f0f0u;  // 16 * codes of weights 4i..4i+3
+    const uint32_t hi = w[i] & 0xf0f0f0f0u;         // 16 * codes of 16+4i..16+4i+3
+    p[2 * i] = perm(0u, lo, kSelB01);
+    p[2 * i + 1] = perm(0u, lo, kSelB23);
+    p[8 + 2 * i] = perm(0u, hi, kSelB01);
+    p[8 + 2 * i + 1] = perm(0u, hi, kSelB23);
+  }
+}
+
 template <>
 __device__ __forceinline__ void unpack<5>(const uint32_t (&w)[5],
                                           uint32_t (&p)[16]) {
@@ -314,7 +328,9 @@ namespace svq {
 // weight stream) do not delay the first LDS writes. Batch entries past the end
 // re-write the last piece with the same data, so every loaded register is
 // consumed on every path.
-template <int QT, int M, int THREADS, int SB>
+// SxMul multiplies the offset term: 16 for a kernel that places every Q4_0
+// code as 16 * code (both nibble halves scaled alike).
+template <int QT, int M, int THREADS, int SB, int SxMul = 1>
 struct XStager {
   using T = QTraits<QT>;
   static constexpr int P = T::kUnitWeights / 8;
@@ -366,7 +382,7 @@ struct XStager {
         sx = dot2(w.z, ones, sx);
         sx = dot2(w.w, ones, sx);
       }
-      sxs[m * stride + u] = sx * T::kSxScale;
+      sxs[m * stride + u] = sx * (T::kSxScale * SxMul);
     }
     __syncthreads();
   }

@@ -52,6 +52,12 @@ const void* mfma_kernel(int qtype, int m, int rows);
 hipError_t launch_gemv_mfma(const GemvArgs& a, int qtype, int m, int rows, int groups,
                             hipStream_t stream);
 
+// Streaming MFMA kernel (svq_gemv_mfma4.hip), 1 <= M <= 4: function pointer
+// and launcher (LDS layout and size as the vector streaming kernel).
+const void* mfma4_kernel(int qtype, int m, int rows);
+hipError_t launch_gemv_mfma4(const GemvArgs& a, int qtype, int m, int rows, int groups,
+                             hipStream_t stream);
+
 hipError_t launch_dequant(const uint8_t* q, const uint16_t* s, void* out,
                           int64_t nblocks, int qtype, int out_dtype,
                           hipStream_t stream);

@@ -201,12 +201,14 @@ def decoder_cases():
     return cases
 
 
-@pytest.mark.parametrize("kernel_path", ["auto", "mfma"], indirect=True)
+@pytest.mark.parametrize("kernel_path", ["auto", "mfma", "mfma4"], indirect=True)
 @pytest.mark.parametrize("qtype,n,k,m,has_bias", decoder_cases())
 def test_gemv_decoder_shapes(cuda_device, kernel_path, qtype, n, k, m, has_bias):
     say(f"gemv decoder shape {kernel_path} {qtype} m={m} n={n} k={k} bias={has_bias}")
     if kernel_path == "mfma":
         assert native.gemv_plan(m, n, k, qtype)["kernel"] == "mfma"
+    if kernel_path == "mfma4" and m <= 4:
+        assert native.gemv_plan(m, n, k, qtype)["kernel"] == "mfma4"
     q, s = gpu_soa(qtype, n, k, seed=n + k + m, dev=cuda_device)
     g = torch.Generator(device=cuda_device).manual_seed(m)
     x = torch.randn((m, k), generator=g, device=cuda_device).half()
@@ -272,16 +274,25 @@ def mfma_eligible(qtype, m, n, k):
     return kb % bps == 0 and lds <= 156 * 1024
 
 
-@pytest.mark.parametrize("kernel_path", ["mfma", "stream", "chunked"], indirect=True)
+def stream_eligible(qtype, m, n, k):
+    """Shapes the streaming kernels take: x and its offset sums in LDS."""
+    units = k // 32 * (2 if qtype == "Q8_0" else 1)
+    per_unit = (16 if qtype == "Q8_0" else 32) * 2 + 4
+    return m * units * per_unit <= 156 * 1024
+
+
+@pytest.mark.parametrize("kernel_path", ["mfma4", "mfma", "stream", "chunked"], indirect=True)
 @pytest.mark.parametrize("qtype", QTYPES)
 def test_gemv_every_kernel_against_oracle(cuda_device, kernel_path, qtype):
     rng = np.random.default_rng(7)
-    for m in (1, 2, 3, 8):
+    for m in (1, 2, 3, 4, 8):
         for n, k in ((1, 32), (13, 128), (33, 192), (129, 2048), (515, 4608), (40, 18432)):
             say(f"gemv {kernel_path} {qtype} m={m} n={n} k={k}")
+            plan = native.gemv_plan(m, n, k, qtype)
             if kernel_path == "mfma":
-                plan = native.gemv_plan(m, n, k, qtype)
                 assert (plan["kernel"] == "mfma") == mfma_eligible(qtype, m, n, k), plan
+            if kernel_path == "mfma4":
+                assert (plan["kernel"] == "mfma4") == (m <= 4 and stream_eligible(qtype, m, n, k)), plan
             q, s = orc.synthetic_soa(qtype, n, k, seed=n + k + m)
             x = rng.standard_normal((m, k)).astype(np.float16)
             bias = rng.standard_normal(n).astype(np.float16)
@@ -340,3 +351,27 @@ def test_gemv_every_mfma_launch_shape(cuda_device, monkeypatch, rows, ksplit):
                 y16 = hip_gemv(to_dev(x, cuda_device), to_dev(q, cuda_device), to_dev(s, cuda_device),
                                qtype, n, to_dev(bias, cuda_device), torch.float16)
                 assert orc.rel_err(y16.float().cpu().numpy(), ref) <= FP16_TOL
+
+
+@pytest.mark.parametrize("rows", (1, 2, 3))
+def test_gemv_mfma4_row_sets(cuda_device, monkeypatch, rows):
+    """Every variant of the streaming MFMA kernel on ragged shapes (3: three
+    consecutive Q5_0 units per lane, for K a multiple of 1536)."""
+    monkeypatch.setenv("SVQ_PATH", "mfma4")
+    monkeypatch.setenv("SVQ_MFMA_R", str(rows))
+    rng = np.random.default_rng(rows)
+    for qtype in QTYPES:
+        shapes = ((1, 77, 320), (2, 130, 1056), (3, 3, 96), (4, 261, 2048))
+        if rows == 3:
+            shapes = ((1, 77, 1536), (2, 130, 4608), (3, 3, 3072), (4, 261, 1536))
+        for m, n, k in shapes:
+            say(f"gemv mfma4 rows={rows} {qtype} m={m} n={n} k={k}")
+            want = rows if rows != 3 or qtype == "Q5_0" else 2
+            assert native.gemv_plan(m, n, k, qtype)["rows"] == want
+            q, s = orc.synthetic_soa(qtype, n, k, seed=m * n + k)
+            x = rng.standard_normal((m, k)).astype(np.float16)
+            bias = rng.standard_normal(n).astype(np.float16)
+            ref = orc.gemv_ref(x, q, s, qtype, n, k, bias)
+            y = hip_gemv(to_dev(x, cuda_device), to_dev(q, cuda_device), to_dev(s, cuda_device), qtype, n,
+                         to_dev(bias, cuda_device), torch.float32)
+            assert orc.rel_err(y.cpu().numpy(), ref) <= FP32_TOL, (rows, qtype, m, n, k)
