@@ -195,58 +195,72 @@ bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out
 
 constexpr int kMfmaMinRows = 5;  // smallest M sent to the MFMA kernel by default
 
-// MFMA launch: 16-row tiles, split along K until tiles x splits give about
-// 16 waves per CU (each split keeping >= 2 steps), persistent workgroups
-// trimmed so that each processes the same number of tile groups. Returns false
-// when the shape or alignment does not suit the kernel: K must be a whole
-// number of steps (4 blocks, 2 for Q8_0), the scales 4-byte aligned, x and
-// its offset sums must fit in LDS, and the arrays below 2^31 bytes.
-// Streaming MFMA launch (M <= 4): row tiles of 4 * R rows over 16 unit
-// slots; two row sets per lane first (each x read serves both), one when that
-// leaves fewer tiles than resident waves; persistent waves trimmed to equal
-// tile counts, as for the vector streaming kernel.
+// Streaming MFMA launch (M <= 4): row tiles of 4 rows (8 with two row sets
+// per lane) over 16 unit slots. Variant (the `rows` code): 3 = Q5_0 with
+// three consecutive units per lane (needs units % 48 == 0), 2 = two row sets
+// per lane, 1 = one. The 4 waves of a workgroup split K (S = 2 or 4) and add
+// their partial sums through LDS: by default S = 2 when the tiles fill a
+// quarter of the resident waves or fewer, otherwise as SVQ_MFMA_S asks. Workgroups are
+// persistent over tile groups, trimmed so that each processes the same number
+// of groups.
 bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_out,
-                  int* waves_out, int* groups_out, int* wmax_out) {
+                  int* ksplit_out, int* groups_out, int* wmax_out) {
   if ((tu.path != 4 && tu.path != 0) || m > 4) return false;
   // Automatic choice (measured at the StarCoder2-8B and GPTBigCode-1B shapes):
   // the matrix-core path wins for Q5_0 at every M and for Q4_0 / Q8_0 from
   // M = 2; at M = 1 the vector path's dot products are cheap enough.
   if (tu.path == 0 && qtype != SVQ_Q5_0 && m < 2) return false;
-  const size_t lds = svq::stream_lds_bytes(qtype, m, k);
   const uint64_t q_bytes = (uint64_t)n * (k / 32) * payload_bytes(qtype);
-  if (lds > kStreamLdsMax || q_bytes >= (1ull << 31) || (uint64_t)n * (k / 16) >= (1ull << 31))
-    return false;
+  if (q_bytes >= (1ull << 31) || (uint64_t)n * (k / 16) >= (1ull << 31)) return false;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   const int cus = device_cus(dev);
   const int wpg = svq::kStreamWavesPerGroup;
-  // Variants (the `rows` code): 3 = Q5_0 with three consecutive units per
-  // lane (needs units % 48 == 0), 2 = two row sets per lane, 1 = one.
   const int units = (k / 32) * svq::units_per_block(qtype);
   const bool triple = qtype == SVQ_Q5_0 && units % 48 == 0;
-  int rows = tu.mfma_r ? tu.mfma_r : (triple ? 3 : 2), wmax = 0, tiles = 0;
+  int rows = tu.mfma_r ? tu.mfma_r : (triple ? 3 : 2);
   if (rows == 3 && !triple) rows = 2;
+  int wmax = 0, tiles = 0;
+  size_t lds = 0;
   for (;;) {
+    lds = svq::mfma4_lds_bytes(qtype, m, k, rows, 4);
+    if (lds > kStreamLdsMax) return false;
     wmax = cus * waves_per_cu(dev, svq::mfma4_kernel(qtype, m, rows), wpg, lds);
     const int tile_rows = rows == 2 ? 8 : 4;
     tiles = (n + tile_rows - 1) / tile_rows;
     if (tiles >= wmax || rows != 2 || tu.mfma_r) break;
     rows = 1;
   }
-  // Long rows with too few tiles to fill the GPU: 16 unit slots per row leave
-  // waves that are long and few; the vector kernel spreads a row over 64 lanes.
+  // Long rows with too few tiles to fill the GPU go to the vector kernel,
+  // which spreads a row over 64 lanes: measured faster than splitting K here.
   if (tu.path == 0 && k > 8192 && tiles < wmax) return false;
-  int waves = tiles < wmax ? tiles : wmax;
-  const int rounds = (tiles + waves - 1) / waves;
-  const int balanced = (tiles + rounds - 1) / rounds;
-  if (balanced >= wmax - wmax / 16) waves = balanced;
+  const int steps = (units + 16 * (rows == 3 ? 3 : 1) - 1) / (16 * (rows == 3 ? 3 : 1));
+  int ksplit = 1;
+  if (tu.mfma_s == 2 || tu.mfma_s == 4) {
+    ksplit = tu.mfma_s;
+  } else if (tu.mfma_s == 0 && 4 * (int64_t)tiles <= wmax && steps >= 8) {
+    ksplit = 2;  // a quarter of the waves or fewer: halve K per wave
+  }
+  if (ksplit > steps) ksplit = 1;  // every wave needs at least one step
+  const int slots = wpg / ksplit;
+  const int tile_groups = (tiles + slots - 1) / slots;
+  const int cap = wmax / wpg;
+  int groups = tile_groups < cap ? tile_groups : cap;
+  const int rounds = (tile_groups + groups - 1) / groups;
+  groups = (tile_groups + rounds - 1) / rounds;
   *rows_out = rows;
-  *waves_out = waves;
-  *groups_out = (waves + wpg - 1) / wpg;
+  *ksplit_out = ksplit;
+  *groups_out = groups;
   *wmax_out = wmax;
   return true;
 }
 
+// MFMA launch: 16-row tiles, split along K until tiles x splits give about
+// 16 waves per CU (each split keeping >= 2 steps), persistent workgroups
+// trimmed so that each processes the same number of tile groups. Returns false
+// when the shape or alignment does not suit the kernel: K must be a whole
+// number of steps (4 blocks, 2 for Q8_0), the scales 4-byte aligned, x and
+// its offset sums must fit in LDS, and the arrays below 2^31 bytes.
 bool choose_mfma(int m, int n, int k, int qtype, const Tuning& tu, const void* s, int* rows_out,
                  int* slots_out, int* ksplit_out, int* groups_out) {
   if (tu.path == 1 || tu.path == 2 || tu.path == 4) return false;
@@ -334,8 +348,8 @@ int svq_gemv(const void* x, const uint8_t* q, const uint16_t* s,
   int lg = 0, rows = 0, wpg = 0, waves = 0, groups = 0, slots = 0, ksplit = 0;
   hipError_t e;
   int wmax = 0;
-  if (choose_mfma4(m, n, k, qtype, tu, &rows, &waves, &groups, &wmax)) {
-    a.waves = waves;
+  if (choose_mfma4(m, n, k, qtype, tu, &rows, &ksplit, &groups, &wmax)) {
+    a.ksplit = ksplit;
     e = svq::launch_gemv_mfma4(a, qtype, m, rows, groups, static_cast<hipStream_t>(stream));
   } else if (choose_mfma(m, n, k, qtype, tu, s, &rows, &slots, &ksplit, &groups)) {
     a.slots = slots;
@@ -365,8 +379,9 @@ int svq_gemv_plan(int m, int n, int k, int qtype, int32_t* plan) {
   int lg = 0, rows = 0, wpg = 0, waves = 0, groups = 0, wmax = 0;
   for (int i = 0; i < 8; ++i) plan[i] = 0;
   int slots = 0, ksplit = 0;
-  if (choose_mfma4(m, n, k, qtype, tu, &rows, &waves, &groups, &wmax)) {
-    const int32_t p[8] = {4, 4, rows, svq::kStreamWavesPerGroup, waves, groups, wmax, 0};
+  if (choose_mfma4(m, n, k, qtype, tu, &rows, &ksplit, &groups, &wmax)) {
+    const int32_t p[8] = {4, ksplit, rows, svq::kStreamWavesPerGroup,
+                          groups * svq::kStreamWavesPerGroup, groups, wmax, 0};
     for (int i = 0; i < 8; ++i) plan[i] = p[i];
   } else if (choose_mfma(m, n, k, qtype, tu, nullptr, &rows, &slots, &ksplit, &groups)) {
     const int32_t p[8] = {3, ksplit, rows, slots * ksplit, groups * slots * ksplit, groups, slots,

@@ -87,7 +87,6 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   static_assert(U == 1 || (U == 3 && QT == 5), "three units per lane: Q5_0 only");
   using T = QTraits<QT>;
   constexpr int kWordsU = U == 3 ? 15 : T::kWords;  // payload dwords per lane per step
-  constexpr int P = T::kUnitWeights / 8;  // 16-byte x pieces per unit
   constexpr int J = T::kUnitWeights / 4;  // MFMAs per unit
   extern __shared__ u32x4 lds[];
   __shared__ u32x2 q5_table[QT == 5 ? 256 : 1];
@@ -100,13 +99,21 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   const int slot = lane >> 2;  // MFMA block: the unit slot of this lane
   const int ri = lane & 3;     // row of the row set; also the A row it supplies
   const int m_a = ri % M;      // activation row it supplies (rows >= M repeat)
+  // Work split: the WPG waves of a workgroup are P tile slots x S K-ranges;
+  // workgroup g processes tile groups g, g + G, ... (P tiles each), and wave
+  // (p, sk) streams steps [st0, st1) of tile p of each group. With S > 1 the
+  // S partial sums of a tile meet in LDS at the end of its group.
+  const int S = a.ksplit, P = WPG / S;
+  const int p_id = wave / S, sk = wave % S;
   const int tile_rows = 4 * R;
   const int tiles = (n + tile_rows - 1) / tile_rows;
-  const int W = a.waves;
-  const int wid = blockIdx.x * WPG + wave;
-  const int my_tiles = wid < W ? (tiles - wid + W - 1) / W : 0;
-  const int niter = (units + kSlots * U - 1) / (kSlots * U);
-  const int steps = my_tiles * niter;
+  const int groups = (tiles + P - 1) / P;
+  const int G = gridDim.x;
+  const int my_tiles = (int)blockIdx.x < groups ? (groups - (int)blockIdx.x + G - 1) / G : 0;
+  const int niter_all = (units + kSlots * U - 1) / (kSlots * U);
+  const int st0 = sk * niter_all / S, st1 = (sk + 1) * niter_all / S;
+  const int steps = my_tiles * (st1 - st0);
+  auto tile_of = [&](int j) { return ((int)blockIdx.x + j * G) * P + p_id; };
   const uint32_t row_bytes = (uint32_t)kb * T::kBlockQ;
 
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)n * row_bytes);
@@ -114,8 +121,10 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bias, a.bias ? (uint32_t)n * 2u : 0u);
 
   if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
+  constexpr int XP = T::kUnitWeights / 8;  // 16-byte x pieces per unit
   u32x4* xs = lds;
-  float* sxs = reinterpret_cast<float*>(xs + M * P * units);
+  float* sxs = reinterpret_cast<float*>(xs + M * XP * units);
+  float* part = sxs + M * units;  // [2][WPG][R][M][4] split-K partial sums
 
   // Row offsets of this lane's R rows in tile `tile` (rows past n: out of
   // range, so they load zeros).
@@ -133,9 +142,9 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 
   uint32_t w[D][R][kWordsU];
   uint32_t sc[D][R][U == 3 ? 2 : 1];
-  int pj = 0, pit = 0;
+  int pj = 0, pit = st0;
   uint32_t pqo[R], pso[R];
-  row_offsets(wid, pqo, pso);
+  row_offsets(tile_of(0), pqo, pso);
   auto issue = [&](int d) {
     const int u = U * (slot + pit * kSlots);
     const bool valid = pj < my_tiles && u < units;
@@ -164,10 +173,10 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
             sr, pso[r] + (uint32_t)(u / T::kUnitsPerBlock) * 2u + oob, 0, 0);
       }
     }
-    if (++pit == niter) {
-      pit = 0;
+    if (++pit == st1) {
+      pit = st0;
       ++pj;
-      row_offsets(wid + pj * W, pqo, pso);
+      row_offsets(tile_of(pj), pqo, pso);
     }
   };
 
@@ -189,7 +198,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d);
   uint32_t bias_bits[R];
-  load_bias(wid, bias_bits);
+  load_bias(tile_of(0), bias_bits);
   st.finish(xs, sxs);
 
   float acc[R][M];
@@ -198,7 +207,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
 
-  int cj = 0, cit = 0;
+  int cj = 0, cit = st0;
   for (int s = 0; s < steps; s += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
@@ -207,10 +216,10 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
         for (int q = 0; q < U; ++q) {
           const int u = min(U * (slot + cit * kSlots) + q, units - 1);
           // A: 4 k values of activation row m_a per MFMA (shared by the R rows).
-          uint32_t xa[P * 4];
+          uint32_t xa[XP * 4];
 #pragma unroll
-          for (int p = 0; p < P; ++p) {
-            const u32x4 v = xs[(m_a * P + p) * units + u];
+          for (int p = 0; p < XP; ++p) {
+            const u32x4 v = xs[(m_a * XP + p) * units + u];
             xa[4 * p] = v.x; xa[4 * p + 1] = v.y; xa[4 * p + 2] = v.z; xa[4 * p + 3] = v.w;
           }
           // C: the offset term of every activation row (rows >= M: zero).
@@ -244,14 +253,37 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
         }
       }
       issue(d);  // refill with the step D ahead (out of range past the end)
-      if (s + d < steps && ++cit == niter) {
-        // Tile done: add the 16 unit slots of each row, store, next tile.
-        const int tile = wid + cj * W;
+      if (s + d < steps && ++cit == st1) {
+        // Tile done: add the 16 unit slots of each row (and the S K-ranges),
+        // store, next tile.
+        const int tile = tile_of(cj);
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int m = 0; m < M; ++m) acc[r][m] = slot_sum(acc[r][m]);
-        if (slot == 0) {
+        if (S > 1) {
+          float* buf = part + (cj & 1) * WPG * R * M * 4;
+          if (slot == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+              for (int m = 0; m < M; ++m) buf[((wave * R + r) * M + m) * 4 + ri] = acc[r][m];
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+          __builtin_amdgcn_s_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+          if (sk == 0 && slot == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+              for (int m = 0; m < M; ++m) {
+                float v = 0.f;
+                for (int o = 0; o < S; ++o) v += buf[(((p_id * S + o) * R + r) * M + m) * 4 + ri];
+                acc[r][m] = v;
+              }
+          }
+        }
+        if (slot == 0 && sk == 0) {
 #pragma unroll
           for (int r = 0; r < R; ++r) {
             const int row = tile * tile_rows + r * 4 + ri;
@@ -272,9 +304,9 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
-        cit = 0;
+        cit = st0;
         ++cj;
-        load_bias(wid + cj * W, bias_bits);
+        load_bias(tile_of(cj), bias_bits);
       }
     }
   }
@@ -343,10 +375,16 @@ const void* mfma4_kernel(int qtype, int m, int rows) {
   return fn;
 }
 
+size_t mfma4_lds_bytes(int qtype, int m, int k, int rows, int ksplit) {
+  const size_t part = ksplit > 1 ? (size_t)2 * kStreamWavesPerGroup * (rows == 2 ? 2 : 1) * m * 4 * 4
+                                 : 0;
+  return stream_lds_bytes(qtype, m, k) + part;
+}
+
 hipError_t launch_gemv_mfma4(const GemvArgs& a, int qtype, int m, int rows, int groups,
                              hipStream_t stream) {
-  return mfma4_dispatch(a, qtype, m, rows, groups, stream_lds_bytes(qtype, m, a.k), stream,
-                        nullptr);
+  return mfma4_dispatch(a, qtype, m, rows, groups, mfma4_lds_bytes(qtype, m, a.k, rows, a.ksplit),
+                        stream, nullptr);
 }
 
 }  // namespace svq

@@ -55,6 +55,7 @@ hipError_t launch_gemv_mfma(const GemvArgs& a, int qtype, int m, int rows, int g
 // Streaming MFMA kernel (svq_gemv_mfma4.hip), 1 <= M <= 4: function pointer
 // and launcher (LDS layout and size as the vector streaming kernel).
 const void* mfma4_kernel(int qtype, int m, int rows);
+size_t mfma4_lds_bytes(int qtype, int m, int k, int rows, int ksplit);
 hipError_t launch_gemv_mfma4(const GemvArgs& a, int qtype, int m, int rows, int groups,
                              hipStream_t stream);
 

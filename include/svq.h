@@ -83,10 +83,11 @@ int svq_gemv(const void *x, const uint8_t *q, const uint16_t *s,
  * Diagnostic with no counterpart in the reference (whose launch tuple is the
  * per-(qtype, M) table SOA_GEMV_CONFIG, quantization.py:121-127): the launch
  * svq_gemv would make for this shape on the current device, as
- * plan[0..7] = {kernel (1 streaming, 2 chunked, 3 MFMA), log2 lanes per row
- * (MFMA: K splits), rows per lane group (MFMA: 16-row tiles per wave), waves
- * per workgroup, waves, workgroups, resident-wave capacity used for the
- * choice (MFMA: tile slots per workgroup), chunk units (chunked only)}.
+ * plan[0..7] = {kernel (1 streaming, 2 chunked, 3 MFMA 16x16x32, 4 MFMA
+ * 4x4x4), log2 lanes per row (MFMA: K splits), rows per lane group (MFMA
+ * 16x16x32: 16-row tiles per wave; MFMA 4x4x4: rows per lane), waves per
+ * workgroup, waves, workgroups, resident-wave capacity used for the choice
+ * (MFMA: tile slots per workgroup), chunk units (chunked only)}.
  * Queries device attributes; launches nothing.
  */
 int svq_gemv_plan(int m, int n, int k, int qtype, int32_t *plan);

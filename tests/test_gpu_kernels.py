@@ -375,3 +375,26 @@ def test_gemv_mfma4_row_sets(cuda_device, monkeypatch, rows):
             y = hip_gemv(to_dev(x, cuda_device), to_dev(q, cuda_device), to_dev(s, cuda_device), qtype, n,
                          to_dev(bias, cuda_device), torch.float32)
             assert orc.rel_err(y.cpu().numpy(), ref) <= FP32_TOL, (rows, qtype, m, n, k)
+
+
+@pytest.mark.parametrize("ksplit", (1, 2, 4))
+@pytest.mark.parametrize("rows", (1, 2, 3))
+def test_gemv_mfma4_ksplit(cuda_device, monkeypatch, rows, ksplit):
+    """Split-K of the streaming MFMA kernel (waves of a workgroup sharing a
+    tile and adding their partial sums in LDS), every variant, ragged rows."""
+    monkeypatch.setenv("SVQ_PATH", "mfma4")
+    monkeypatch.setenv("SVQ_MFMA_R", str(rows))
+    monkeypatch.setenv("SVQ_MFMA_S", str(ksplit))
+    rng = np.random.default_rng(10 * rows + ksplit)
+    for qtype in QTYPES:
+        for m, n, k in ((1, 37, 1536), (2, 130, 4608), (3, 9, 18432)):
+            plan = native.gemv_plan(m, n, k, qtype)
+            say(f"gemv mfma4 rows={rows} ksplit={ksplit} {qtype} m={m} n={n} k={k} plan={plan}")
+            assert plan["kernel"] == "mfma4" and plan["lg_g"] in (1, ksplit), plan
+            q, s = orc.synthetic_soa(qtype, n, k, seed=m + n + k)
+            x = rng.standard_normal((m, k)).astype(np.float16)
+            bias = rng.standard_normal(n).astype(np.float16)
+            ref = orc.gemv_ref(x, q, s, qtype, n, k, bias)
+            y = hip_gemv(to_dev(x, cuda_device), to_dev(q, cuda_device), to_dev(s, cuda_device), qtype, n,
+                         to_dev(bias, cuda_device), torch.float32)
+            assert orc.rel_err(y.cpu().numpy(), ref) <= FP32_TOL, (rows, ksplit, qtype, m, n, k)
