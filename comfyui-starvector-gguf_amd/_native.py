@@ -58,6 +58,11 @@ def load() -> ctypes.CDLL:
         lib.svq_dequant.restype = i32
         lib.svq_dequant_rows.argtypes = [vp, vp, vp, i64, i64, i32, vp, i32, i32, vp]
         lib.svq_dequant_rows.restype = i32
+        lib.svq_decode_attention_workspace.argtypes = [i32, i32, i32, i32]
+        lib.svq_decode_attention_workspace.restype = i64
+        lib.svq_decode_attention.argtypes = [vp, i64, vp, vp, vp, vp, i64, vp, vp, i32, vp,
+                                             i32, i32, i32, i32, ctypes.c_float, vp, i64, vp]
+        lib.svq_decode_attention.restype = i32
         version = lib.svq_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"libsvq ABI {version}, expected {ABI_VERSION}")
@@ -139,3 +144,63 @@ def dequant_rows(q: torch.Tensor, s: torch.Tensor, ids: torch.Tensor, nrows: int
                                   QTYPE_CODE[qtype], DTYPE_CODE[out.dtype],
                                   _stream(q.device))
     _check(lib, "svq_dequant_rows", rc)
+
+
+_workspaces: dict = {}
+
+
+def attention_workspace(device: torch.device, rows: int, heads: int, kv_heads: int,
+                        span: int) -> torch.Tensor:
+    """A workspace for svq_decode_attention, cached per device and grown as
+    needed. Calls that share it must be ordered (one stream)."""
+    lib = load()
+    need = lib.svq_decode_attention_workspace(rows, heads, kv_heads, span)
+    _check(lib, "svq_decode_attention_workspace", min(need, 0))
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def decode_attention(qkv: torch.Tensor, cos: torch.Tensor | None, sin: torch.Tensor | None,
+                     keys: torch.Tensor, values: torch.Tensor, position: torch.Tensor,
+                     bias: torch.Tensor | None, out: torch.Tensor, heads: int, kv_heads: int,
+                     scale: float, workspace: torch.Tensor) -> None:
+    """One layer's decode attention (svq_decode_attention). qkv [rows, >= (heads +
+    2 kv_heads) * 128] fp16 with unit stride in its last dim; keys/values the
+    layer's cache or a slot-prefix view of it, [rows, kv_heads, span, 128];
+    position a device int64 scalar; out [rows, heads * 128]."""
+    lib = load()
+    if keys.dim() != 4 or values.shape != keys.shape or values.stride() != keys.stride():
+        raise ValueError("keys and values must be [rows, kv_heads, span, head_dim] views "
+                         "of the same layout")
+    rows, span, head_dim = keys.shape[0], keys.shape[2], keys.shape[3]
+    st = keys.stride()
+    if st[3] != 1 or st[2] != head_dim or st[1] % head_dim or st[0] != kv_heads * st[1]:
+        raise ValueError("keys/values must be slot-prefix views of a contiguous "
+                         "[rows, kv_heads, capacity, head_dim] cache")
+    capacity = st[1] // head_dim
+    if qkv.dim() != 2 or qkv.stride(1) != 1 or qkv.shape[0] != rows:
+        raise ValueError("qkv must be [rows, width] with unit stride in its last dim")
+    if not out.is_contiguous() or out.numel() != rows * heads * head_dim:
+        raise ValueError("out must be a contiguous [rows, heads * head_dim] tensor")
+    for name, t in (("cos", cos), ("sin", sin), ("bias", bias)):
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if position.dtype != torch.int64 or position.numel() != 1:
+        raise ValueError("position must be a one-element int64 tensor")
+    tensors = [qkv, keys, values, out, position] + [t for t in (cos, sin, bias) if t is not None]
+    if any(t.dtype != torch.float16 for t in tensors if t is not position):
+        raise ValueError("qkv, keys, values, out, cos, sin and bias must be float16")
+    if any(t.device != qkv.device for t in tensors + [workspace]):
+        raise ValueError("all tensors must be on one device")
+    with _on_device(qkv.device):
+        rc = lib.svq_decode_attention(
+            qkv.data_ptr(), qkv.stride(0), None if cos is None else cos.data_ptr(),
+            None if sin is None else sin.data_ptr(), keys.data_ptr(), values.data_ptr(),
+            capacity, position.data_ptr(), None if bias is None else bias.data_ptr(), span,
+            out.data_ptr(), rows, heads, kv_heads, head_dim, scale, workspace.data_ptr(),
+            workspace.numel(), _stream(qkv.device))
+    _check(lib, "svq_decode_attention", rc)

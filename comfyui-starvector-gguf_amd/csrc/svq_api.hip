@@ -441,4 +441,66 @@ int svq_dequant_rows(const uint8_t* q, const uint16_t* s, const int64_t* ids,
   return 0;
 }
 
+int64_t svq_decode_attention_workspace(int rows, int heads, int kv_heads, int span) {
+  if (rows < 1 || kv_heads < 1 || heads < kv_heads || heads % kv_heads != 0 ||
+      heads / kv_heads > SVQ_MAX_GROUP || span < 1)
+    return fail(SVQ_E_SHAPE, "invalid attention shape rows=%d heads=%d kv_heads=%d span=%d",
+                rows, heads, kv_heads, span);
+  return svq::attention_workspace_bytes(rows, heads, kv_heads, span);
+}
+
+int svq_decode_attention(const uint16_t* qkv, int64_t qkv_stride, const uint16_t* cos,
+                         const uint16_t* sin, uint16_t* keys, uint16_t* values,
+                         int64_t capacity, const int64_t* position, const uint16_t* bias,
+                         int span, uint16_t* out, int rows, int heads, int kv_heads,
+                         int head_dim, float scale, void* workspace,
+                         int64_t workspace_bytes, void* stream) {
+  if (rows < 1 || kv_heads < 1 || heads < kv_heads || heads % kv_heads != 0 ||
+      heads / kv_heads > SVQ_MAX_GROUP || head_dim != SVQ_HEAD_DIM || span < 1 ||
+      capacity < span || rows * (int64_t)kv_heads > 65535 ||
+      qkv_stride < (int64_t)(heads + 2 * kv_heads) * head_dim || qkv_stride % 8 != 0)
+    return fail(SVQ_E_SHAPE,
+                "invalid attention shape rows=%d heads=%d kv_heads=%d head_dim=%d span=%d "
+                "capacity=%lld qkv_stride=%lld",
+                rows, heads, kv_heads, head_dim, span, (long long)capacity,
+                (long long)qkv_stride);
+  if ((int64_t)span * head_dim * 2 >= ((int64_t)1 << 31) ||
+      rows * (int64_t)kv_heads * capacity * head_dim >= ((int64_t)1 << 40))
+    return fail(SVQ_E_RANGE, "attention cache too large");
+  if (!qkv || !keys || !values || !position || !out || !workspace)
+    return fail(SVQ_E_NULL, "NULL qkv, keys, values, position, out or workspace");
+  if ((cos == nullptr) != (sin == nullptr))
+    return fail(SVQ_E_NULL, "cos and sin must both be given or both be NULL");
+  if (!aligned(qkv, 16) || !aligned(keys, 16) || !aligned(values, 16) || !aligned(out, 16) ||
+      (cos && (!aligned(cos, 16) || !aligned(sin, 16))) || (bias && !aligned(bias, 2)) ||
+      !aligned(position, 8) || !aligned(workspace, 256))
+    return fail(SVQ_E_ALIGN, "misaligned attention argument");
+  const int64_t need = svq::attention_workspace_bytes(rows, heads, kv_heads, span);
+  if (workspace_bytes < need)
+    return fail(SVQ_E_WORKSPACE, "workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)need);
+  svq::AttnArgs a{};
+  a.qkv = qkv;
+  a.qkv_stride = qkv_stride;
+  a.cos = cos;
+  a.sin = sin;
+  a.keys = keys;
+  a.values = values;
+  a.capacity = capacity;
+  a.position = position;
+  a.bias = bias;
+  a.span = span;
+  a.out = out;
+  a.kv_heads = kv_heads;
+  a.scale = scale;
+  a.nchunks = svq::attention_chunks(span);
+  a.ml = static_cast<float2*>(workspace);
+  a.acc = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                   svq::attention_ml_bytes(rows, heads, span));
+  const hipError_t e = svq::launch_decode_attention(a, rows, heads / kv_heads,
+                                                    static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "svq_decode_attention launch");
+  return 0;
+}
+
 }  // extern "C"

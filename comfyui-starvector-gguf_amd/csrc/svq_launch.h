@@ -59,6 +59,39 @@ size_t mfma4_lds_bytes(int qtype, int m, int k, int rows, int ksplit);
 hipError_t launch_gemv_mfma4(const GemvArgs& a, int qtype, int m, int rows, int groups,
                              hipStream_t stream);
 
+// Decode attention (svq_attention.hip): one new token per row against a
+// [rows, kv_heads, capacity, 128] fp16 key/value cache.
+struct AttnArgs {
+  const uint16_t* qkv;     // fp16 [rows, qkv_stride]: q (heads x 128), k, v (kv_heads x 128 each)
+  int64_t qkv_stride;      // elements between rows of qkv
+  const uint16_t* cos;     // fp16 [128] rotary tables, or nullptr (no rotation)
+  const uint16_t* sin;
+  uint16_t* keys;          // fp16 cache of this layer
+  uint16_t* values;
+  int64_t capacity;        // slots per (row, kv head) in the cache
+  const int64_t* position; // device scalar: the slot of the new token
+  const uint16_t* bias;    // fp16 [span] additive score bias, or nullptr
+  int span;                // slots attended
+  uint16_t* out;           // fp16 [rows, heads x 128]
+  int kv_heads;
+  float scale;             // score scale (head_dim^-0.5)
+  float2* ml;              // workspace: (max score, sum of exponentials) per head and chunk
+  float* acc;              // workspace: weighted sum of V [128] per head and chunk
+  int nchunks;
+};
+// Merge of the chunk partials (second kernel of the attention).
+struct AttnMerge {
+  const float2* ml;
+  const float* acc;
+  uint16_t* out;
+  int nchunks;
+};
+int attention_chunks(int span);
+int64_t attention_ml_bytes(int rows, int heads, int span);
+hipError_t launch_chunks(const AttnArgs& a, int rows, int group, hipStream_t stream);
+int64_t attention_workspace_bytes(int rows, int heads, int kv_heads, int span);
+hipError_t launch_decode_attention(const AttnArgs& a, int rows, int group, hipStream_t stream);
+
 hipError_t launch_dequant(const uint8_t* q, const uint16_t* s, void* out,
                           int64_t nblocks, int qtype, int out_dtype,
                           hipStream_t stream);

@@ -6,8 +6,10 @@ runtime_shared.py (CachedDecoding :345-394) and its beam sampling
 (_penalize/_warp/_beam_sample :170-265). Every quantized linear is a
 `GGUFLinear` over SoA arrays, so each decode step runs the HIP GEMV 4 x layers
 + 1 times (q, k and v are one fused linear: their SoA rows concatenated, a pure
-byte concatenation). Attention, LayerNorm, RoPE, sampling and the KV cache
-stay in PyTorch.
+byte concatenation). On the GPU a decode step's attention (rotation of q and
+k, the cache write and grouped-query attention over the cache) is one HIP
+kernel per layer (`svq_decode_attention`). Prefill attention, LayerNorm,
+sampling and host decoding use PyTorch ops.
 
 Attention products are arranged so that no batched product takes a transposed
 view as its right operand: decode computes K @ q^T with a contiguous q^T, and
@@ -22,6 +24,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from . import _native as native
 from .quantization import BLOCK_BYTES, GGUFEmbedding, GGUFLinear, tied_head
 
 # Sampling settings of the reference (runtime_shared.py:148-150).
@@ -109,6 +112,26 @@ class Starcoder2Block(nn.Module):
         hd, heads, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
         rows, length, hidden = x.shape
         qkv = self.qkv_proj(self.input_layernorm(x))
+        if position is not None and x.is_cuda:
+            # Rotation, cache write and attention in one HIP kernel.
+            out = torch.empty((rows, hidden), dtype=x.dtype, device=x.device)
+            workspace = native.attention_workspace(x.device, rows, heads, kvh, keys.shape[2])
+            native.decode_attention(qkv.view(rows, -1), cos.view(-1), sin.view(-1), keys,
+                                    values, position, bias, out, heads, kvh, hd ** -0.5,
+                                    workspace)
+            out = out.view(rows, 1, hidden)
+        else:
+            out = self.torch_attention(qkv, cos, sin, keys, values, position, bias)
+        x = x + self.o_proj(out)
+        return x + self.c_proj(F.gelu(self.c_fc(self.post_attention_layernorm(x)), approximate="tanh"))
+
+    def torch_attention(self, qkv, cos, sin, keys, values, position=None, bias=None):
+        """The reference's attention ops (runtime_8b.py:38-55) in torch: prefill
+        on any device (position None) and decode on the host."""
+        cfg = self.cfg
+        hd, heads, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
+        rows, length, _ = qkv.shape
+        hidden = heads * hd
         q, k, v = qkv.split((hidden, kvh * hd, kvh * hd), -1)
         q = rotate(q.view(rows, length, heads, hd).transpose(1, 2), cos, sin)
         k = rotate(k.view(rows, length, kvh, hd).transpose(1, 2), cos, sin)
@@ -117,20 +140,15 @@ class Starcoder2Block(nn.Module):
         if position is None:
             keys[:, :, :length] = k
             values[:, :, :length] = v
-            out = causal_attention(q, k, v, group).reshape(rows, length, hidden)
-        else:
-            keys.index_copy_(2, position, k)
-            values.index_copy_(2, position, v)
-            span = keys.shape[2]
-            # scores^T = K @ q^T per (row, kv head): [span, hd] @ [hd, group].
-            kb = keys.flatten(0, 1)
-            qt = q.reshape(rows * kvh, group, hd).transpose(1, 2).contiguous()
-            scores = torch.bmm(kb, qt).transpose(1, 2) * hd ** -0.5 + bias
-            probs = torch.softmax(scores, -1, dtype=torch.float32).to(x.dtype).contiguous()
-            out = torch.bmm(probs, values.flatten(0, 1)).view(rows, 1, hidden)
-            del span
-        x = x + self.o_proj(out)
-        return x + self.c_proj(F.gelu(self.c_fc(self.post_attention_layernorm(x)), approximate="tanh"))
+            return causal_attention(q, k, v, group).reshape(rows, length, hidden)
+        keys.index_copy_(2, position, k)
+        values.index_copy_(2, position, v)
+        # scores^T = K @ q^T per (row, kv head): [span, hd] @ [hd, group].
+        kb = keys.flatten(0, 1)
+        qt = q.reshape(rows * kvh, group, hd).transpose(1, 2).contiguous()
+        scores = torch.bmm(kb, qt).transpose(1, 2) * hd ** -0.5 + bias
+        probs = torch.softmax(scores, -1, dtype=torch.float32).to(qkv.dtype).contiguous()
+        return torch.bmm(probs, values.flatten(0, 1)).view(rows, 1, hidden)
 
 
 def causal_attention(q, k, v, group):
@@ -225,6 +243,12 @@ class CachedDecoding:
         self.tokens = torch.zeros(keys.shape[1], dtype=torch.long, device=keys.device)
         self.position = torch.full((1,), length, dtype=torch.long, device=keys.device)
         self.graphs = {}
+        if keys.is_cuda:
+            # Allocated here, outside any capture, for the largest span; the
+            # decode steps reuse it.
+            cfg = model.cfg
+            native.attention_workspace(keys.device, keys.shape[1], cfg.heads, cfg.kv_heads,
+                                       keys.shape[3])
 
     def span(self):
         return min(self.keys.shape[-2], max(512, 1 << self.length.bit_length()))

@@ -1,5 +1,6 @@
 /*
- * svq.h - C ABI of the gfx950 GGUF SoA dequantize + GEMV library (libsvq.so).
+ * svq.h - C ABI of the gfx950 GGUF SoA dequantize + GEMV library (libsvq.so),
+ * with the fused decode attention of the decoder layers around it.
  *
  * Weights use the structure-of-arrays layout that the reference builds at load
  * time (quantization.py:67-90, `pack_gguf_soa`): for an N x K matrix with
@@ -54,6 +55,10 @@ extern "C" {
 #define SVQ_E_RANGE (-5)   /* a size exceeds the 32-bit offsets the kernels use */
 #define SVQ_E_ALIGN (-6)   /* x / q / out not aligned for 16-byte accesses
                               (q: 4 bytes for Q5_0; s, bias: 2 bytes) */
+#define SVQ_E_WORKSPACE (-7) /* workspace smaller than the call needs */
+
+#define SVQ_HEAD_DIM 128 /* head dimension of svq_decode_attention */
+#define SVQ_MAX_GROUP 16 /* largest query heads per key/value head */
 
 /* Version of this ABI (SVQ_ABI_VERSION). */
 int svq_abi_version(void);
@@ -109,6 +114,42 @@ int svq_dequant(const uint8_t *q, const uint16_t *s, void *out,
 int svq_dequant_rows(const uint8_t *q, const uint16_t *s, const int64_t *ids,
                      int64_t nids, int64_t nrows, int k, void *out,
                      int qtype, int out_dtype, void *stream);
+
+/*
+ * Bytes of workspace svq_decode_attention needs for this shape (a negative
+ * SVQ_E* code for an invalid one): the per-chunk partial results of the
+ * attention, written and read within one call (no initialization needed).
+ * Calls that share one workspace must not overlap (same stream, or ordered by
+ * events).
+ */
+int64_t svq_decode_attention_workspace(int rows, int heads, int kv_heads, int span);
+
+/*
+ * Decode attention of one layer for one new token per row, fused with the
+ * rotary embedding and the cache write. Replaces the decode branch of the
+ * reference blocks: StarCoder2 (runtime_8b.py:38-55: `_rotate` of q and k,
+ * `index_copy_` of k and v into slot `position`, `baddbmm` with the bias and
+ * alpha = head_dim^-0.5, fp32 softmax, `bmm` with V) and GPTBigCode
+ * multi-query (runtime_1b.py:30-45: no rotation, kv_heads = 1).
+ *   qkv       fp16 [rows, qkv_stride]: q (heads x 128), then k and v
+ *             (kv_heads x 128 each), as a fused q/k/v projection writes them
+ *   cos, sin  fp16 [128] rotary tables of the position, or both NULL
+ *   keys, values  fp16 [rows, kv_heads, capacity, 128] cache of this layer;
+ *             slot *position of every (row, kv head) receives the new k / v
+ *   position  device int64 scalar, 0 <= *position < span (a slot outside
+ *             [0, span) is neither written nor attended)
+ *   bias      fp16 [span] additive score bias (0 / -inf masks), or NULL
+ *   out       fp16 [rows, heads x 128]
+ * Query head h attends key/value head h / (heads / kv_heads). Scores are
+ * rounded to fp16 as the reference's fp16 baddbmm stores them; softmax and
+ * the weighted sum run in fp32.
+ */
+int svq_decode_attention(const uint16_t *qkv, int64_t qkv_stride, const uint16_t *cos,
+                         const uint16_t *sin, uint16_t *keys, uint16_t *values,
+                         int64_t capacity, const int64_t *position, const uint16_t *bias,
+                         int span, uint16_t *out, int rows, int heads, int kv_heads,
+                         int head_dim, float scale, void *workspace,
+                         int64_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -16,13 +16,15 @@ HEADER = ROOT / "include" / "svq.h"
 
 def declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(svq_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int64_t|int|const char \*)\s*(svq_\w+)\s*\(", text,
+                                  re.M)))
 
 
 def test_header_declares_the_entry_points():
     names = declared_functions()
     assert {"svq_abi_version", "svq_last_error", "svq_gemv", "svq_dequant",
-            "svq_dequant_rows"} <= set(names)
+            "svq_dequant_rows", "svq_decode_attention",
+            "svq_decode_attention_workspace"} <= set(names)
 
 
 def test_library_exports_every_declared_function():
@@ -105,3 +107,43 @@ def test_gemv_plan_rejects_bad_arguments():
     assert lib.svq_gemv_plan(2, 64, 40, 4, plan) == -2
     assert lib.svq_gemv_plan(2, 0, 64, 4, plan) == -2
     assert lib.svq_gemv_plan(2, 64, 64, 4, None) == -3
+
+
+def attention(**kw):
+    args = dict(qkv=FAKE, stride=(36 + 8) * 128, cos=FAKE, sin=FAKE, keys=FAKE, values=FAKE,
+                capacity=64, position=FAKE, bias=FAKE, span=64, out=FAKE, rows=2, heads=36,
+                kv_heads=4, head_dim=128, scale=128 ** -0.5, workspace=FAKE,
+                workspace_bytes=1 << 20)
+    args.update(kw)
+    lib = native.load()
+    return lib.svq_decode_attention(
+        args["qkv"], args["stride"], args["cos"], args["sin"], args["keys"], args["values"],
+        args["capacity"], args["position"], args["bias"], args["span"], args["out"],
+        args["rows"], args["heads"], args["kv_heads"], args["head_dim"], args["scale"],
+        args["workspace"], args["workspace_bytes"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(heads=35), -2), (dict(kv_heads=0), -2), (dict(heads=34, kv_heads=2), -2),
+    (dict(head_dim=64), -2), (dict(span=0), -2), (dict(capacity=32), -2), (dict(rows=0), -2),
+    (dict(stride=44 * 128 - 8), -2), (dict(stride=44 * 128 + 4), -2),
+    (dict(span=1 << 23, capacity=1 << 23), -5),
+    (dict(qkv=None), -3), (dict(keys=None), -3), (dict(position=None), -3),
+    (dict(workspace=None), -3), (dict(cos=None), -3),
+    (dict(qkv=FAKE + 8), -6), (dict(cos=FAKE + 2), -6), (dict(bias=FAKE + 1), -6),
+    (dict(position=FAKE + 4), -6), (dict(workspace=FAKE + 16), -6),
+    (dict(workspace_bytes=1024), -7),
+])
+def test_decode_attention_rejects_bad_arguments(kw, code):
+    assert attention(**kw) == code
+    assert native.load().svq_last_error().decode()
+
+
+def test_decode_attention_workspace_size():
+    lib = native.load()
+    # Per (row, query head) and chunk of 64 slots: (max, sum) as 8 bytes,
+    # padded to 256 bytes in all, then 128 fp32 weighted-V sums.
+    assert lib.svq_decode_attention_workspace(2, 36, 4, 1537) == 14592 + 2 * 36 * 25 * 512
+    assert lib.svq_decode_attention_workspace(2, 16, 1, 64) == 256 + 2 * 16 * 512
+    assert lib.svq_decode_attention_workspace(2, 36, 5, 64) == -2
+    assert lib.svq_decode_attention_workspace(2, 34, 2, 64) == -2  # 17 heads per kv head

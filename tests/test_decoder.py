@@ -17,7 +17,9 @@ import torch
 import starvector_amd.quantization as quantization
 from starvector_amd.decoder import DecoderConfig, Starcoder2Decoder, beam_steps
 
-SMALL = DecoderConfig(hidden=256, heads=4, kv_heads=2, inner=512, layers=2, vocab=320,
+# head_dim 128, as every StarVector decoder (the fused decode attention
+# kernel's head size); 2 query heads per key/value head.
+SMALL = DecoderConfig(hidden=512, heads=4, kv_heads=2, inner=1024, layers=2, vocab=320,
                       window=4096, context=512)
 
 
