@@ -52,6 +52,9 @@ def load() -> ctypes.CDLL:
         lib.svq_last_error.restype = ctypes.c_char_p
         lib.svq_gemv.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
         lib.svq_gemv.restype = i32
+        lib.svq_gemv_fused.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp,
+                                       ctypes.c_float, vp, i32, vp]
+        lib.svq_gemv_fused.restype = i32
         lib.svq_gemv_plan.argtypes = [i32, i32, i32, i32, ctypes.POINTER(ctypes.c_int32)]
         lib.svq_gemv_plan.restype = i32
         lib.svq_dequant.argtypes = [vp, vp, vp, i64, i32, i32, vp]
@@ -108,6 +111,38 @@ def gemv(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, y: torch.Tensor,
                           m, n, k, QTYPE_CODE[qtype], DTYPE_CODE[y.dtype],
                           _stream(x.device))
     _check(lib, "svq_gemv", rc)
+
+
+ACTIVATION_CODE = {None: 0, "gelu_tanh": 1}
+
+
+def gemv_fused(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, y: torch.Tensor,
+               qtype: str, bias: torch.Tensor | None = None,
+               ln_weight: torch.Tensor | None = None, ln_bias: torch.Tensor | None = None,
+               ln_eps: float = 1e-5, residual: torch.Tensor | None = None,
+               activation: str | None = None) -> None:
+    """y = residual + act(x' @ W^T + bias), x' = LayerNorm(x) when ln_weight or
+    ln_bias is given (svq_gemv_fused); fp16 tensors, contiguous, on one GPU."""
+    lib = load()
+    m, k = x.shape
+    n = y.shape[1]
+    for name, t in (("ln_weight", ln_weight), ("ln_bias", ln_bias)):
+        if t is not None and (t.shape != (k,) or t.dtype != torch.float16 or
+                              not t.is_contiguous() or t.device != x.device):
+            raise ValueError(f"{name} must be a contiguous float16 [{k}] tensor on {x.device}")
+    if residual is not None and (residual.shape != y.shape or residual.dtype != torch.float16
+                                 or not residual.is_contiguous() or
+                                 residual.device != x.device):
+        raise ValueError(f"residual must be a contiguous float16 {tuple(y.shape)} tensor")
+    if y.dtype != torch.float16:
+        raise ValueError("svq_gemv_fused writes float16")
+    ptr = lambda t: None if t is None else t.data_ptr()
+    with _on_device(x.device):
+        rc = lib.svq_gemv_fused(x.data_ptr(), q.data_ptr(), s.data_ptr(), ptr(bias),
+                                y.data_ptr(), m, n, k, QTYPE_CODE[qtype], ptr(ln_weight),
+                                ptr(ln_bias), ln_eps, ptr(residual),
+                                ACTIVATION_CODE[activation], _stream(x.device))
+    _check(lib, "svq_gemv_fused", rc)
 
 
 PLAN_FIELDS = ("kernel", "lg_g", "rows", "waves_per_group", "waves", "groups",

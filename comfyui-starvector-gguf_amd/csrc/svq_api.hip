@@ -306,17 +306,19 @@ bool choose_mfma(int m, int n, int k, int qtype, const Tuning& tu, const void* s
   return true;
 }
 
-}  // namespace
+// Fused prologue / epilogue of svq_gemv_fused (all null / zero for svq_gemv).
+struct Fusion {
+  const uint16_t* ln_w = nullptr;
+  const uint16_t* ln_b = nullptr;
+  float ln_eps = 0.f;
+  const uint16_t* residual = nullptr;
+  int act = SVQ_ACT_NONE;
+  bool layer_norm() const { return ln_w || ln_b; }
+};
 
-extern "C" {
-
-int svq_abi_version(void) { return SVQ_ABI_VERSION; }
-
-const char* svq_last_error(void) { return g_error; }
-
-int svq_gemv(const void* x, const uint8_t* q, const uint16_t* s,
-             const uint16_t* bias, void* y, int m, int n, int k, int qtype,
-             int y_dtype, void* stream) {
+int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t* bias,
+              void* y, int m, int n, int k, int qtype, int y_dtype, const Fusion& f,
+              void* stream) {
   if (!valid_qtype(qtype)) return fail(SVQ_E_QTYPE, "unsupported qtype %d", qtype);
   if (m < 1 || m > SVQ_MAX_ROWS)
     return fail(SVQ_E_SHAPE, "m=%d outside 1..%d", m, SVQ_MAX_ROWS);
@@ -345,29 +347,75 @@ int svq_gemv(const void* x, const uint8_t* q, const uint16_t* s,
   a.n = n;
   a.k = k;
   a.y_f32 = y_dtype == SVQ_F32;
+  a.ln_w = f.ln_w;
+  a.ln_b = f.ln_b;
+  a.ln_eps = f.ln_eps;
+  a.residual = f.residual;
+  a.act = f.act;
   int lg = 0, rows = 0, wpg = 0, waves = 0, groups = 0, slots = 0, ksplit = 0;
   hipError_t e;
   int wmax = 0;
+  // The LayerNorm runs in the x staging of the two streaming kernels.
   if (choose_mfma4(m, n, k, qtype, tu, &rows, &ksplit, &groups, &wmax)) {
     a.ksplit = ksplit;
     e = svq::launch_gemv_mfma4(a, qtype, m, rows, groups, static_cast<hipStream_t>(stream));
-  } else if (choose_mfma(m, n, k, qtype, tu, s, &rows, &slots, &ksplit, &groups)) {
+  } else if (!f.layer_norm() &&
+             choose_mfma(m, n, k, qtype, tu, s, &rows, &slots, &ksplit, &groups)) {
     a.slots = slots;
     a.ksplit = ksplit;
     e = svq::launch_gemv_mfma(a, qtype, m, rows, groups, static_cast<hipStream_t>(stream));
-  } else if (choose_stream(m, n, k, qtype, tu, &lg, &rows, &wpg, &waves, &groups)) {
+  } else if (choose_stream(m, n, k, qtype, f.layer_norm() ? Tuning{} : tu, &lg, &rows, &wpg,
+                           &waves, &groups)) {
     a.lg_g = lg;
     a.waves = waves;
     e = svq::launch_gemv_stream(a, qtype, m, rows, wpg, groups,
                                 static_cast<hipStream_t>(stream));
-  } else {
+  } else if (!f.layer_norm()) {
     const svq::GemvShape sh = choose_chunked_shape(m, n, k, qtype, tu);
     a.lg_g = sh.lg_g;
     a.chunk_units = sh.chunk_units;
     e = svq::launch_gemv(a, sh, qtype, static_cast<hipStream_t>(stream));
+  } else {
+    return fail(SVQ_E_SHAPE, "LayerNorm fusion needs x (m=%d, k=%d) to fit in LDS", m, k);
   }
   if (e != hipSuccess) return hip_fail(e, "svq_gemv launch");
   return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int svq_abi_version(void) { return SVQ_ABI_VERSION; }
+
+const char* svq_last_error(void) { return g_error; }
+
+int svq_gemv(const void* x, const uint8_t* q, const uint16_t* s,
+             const uint16_t* bias, void* y, int m, int n, int k, int qtype,
+             int y_dtype, void* stream) {
+  return gemv_impl(x, q, s, bias, y, m, n, k, qtype, y_dtype, Fusion{}, stream);
+}
+
+int svq_gemv_fused(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t* bias,
+                   void* y, int m, int n, int k, int qtype, const uint16_t* ln_weight,
+                   const uint16_t* ln_bias, float ln_eps, const uint16_t* residual,
+                   int activation, void* stream) {
+  if (activation != SVQ_ACT_NONE && activation != SVQ_ACT_GELU_TANH)
+    return fail(SVQ_E_DTYPE, "unsupported activation %d", activation);
+  if ((ln_weight && !aligned(ln_weight, 16)) || (ln_bias && !aligned(ln_bias, 16)) ||
+      (residual && !aligned(residual, 2)))
+    return fail(SVQ_E_ALIGN, "misaligned LayerNorm parameters or residual");
+  if ((ln_weight || ln_bias) && !(ln_eps >= 0.f))
+    return fail(SVQ_E_SHAPE, "invalid LayerNorm eps");
+  if (residual && residual != y && x == y)
+    return fail(SVQ_E_SHAPE, "y must not alias x");
+  Fusion f;
+  f.ln_w = ln_weight;
+  f.ln_b = ln_bias;
+  f.ln_eps = ln_eps;
+  f.residual = residual;
+  f.act = activation;
+  return gemv_impl(x, q, s, bias, y, m, n, k, qtype, SVQ_F16, f, stream);
 }
 
 int svq_gemv_plan(int m, int n, int k, int qtype, int32_t* plan) {

@@ -16,6 +16,8 @@
 
 #include <type_traits>
 
+#include "svq_launch.h"
+
 namespace svq {
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
@@ -316,6 +318,32 @@ __device__ __forceinline__ void load_unit(const uint8_t* p,
 
 namespace svq {
 
+// Sum of v over the G = 1 << lg_g consecutive lanes of a lane group, left in
+// every lane of the group: DPP quad permutes and row mirrors within 16 lanes,
+// then the gfx950 lane-swap instructions across 16- and 32-lane halves. No
+// LDS traffic.
+__device__ __forceinline__ float group_sum(float v, int lg_g) {
+  auto dpp = [](float f, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
+        __builtin_bit_cast(int, f), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  if (lg_g >= 1) v += dpp(v, std::integral_constant<int, 0xb1>{});   // quad_perm [1,0,3,2]
+  if (lg_g >= 2) v += dpp(v, std::integral_constant<int, 0x4e>{});   // quad_perm [2,3,0,1]
+  if (lg_g >= 3) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  if (lg_g >= 4) v += dpp(v, std::integral_constant<int, 0x140>{});  // row_mirror
+  if (lg_g >= 5) {
+    const int i = __builtin_bit_cast(int, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(i, i, false, false);
+    v = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+  }
+  if (lg_g >= 6) {
+    const int i = __builtin_bit_cast(int, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(i, i, false, false);
+    v = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+  }
+  return v;
+}
+
 // Staging of x[:, cu0 : cu0 + cun units] (fp16, all M rows) into LDS in
 // piece-major order, xs[(m * P + p) * stride + u], followed by the per-unit,
 // per-row offset term kSxScale * sum(x over the unit) in sxs[m * stride + u].
@@ -363,6 +391,120 @@ struct XStager {
 
   __device__ __forceinline__ void begin() { load_batch(threadIdx.x); }
 
+  // LayerNorm of every staged row (full rows only: cu0 == 0, cun units = k).
+  const uint16_t* ln_w = nullptr;
+  const uint16_t* ln_b = nullptr;
+  float ln_eps = 0.f;
+  __device__ __forceinline__ void set_layer_norm(const uint16_t* w, const uint16_t* b,
+                                                 float eps) {
+    ln_w = w;
+    ln_b = b;
+    ln_eps = eps;
+  }
+
+  // Piece t of the staged rows in row-major order: its row, its LDS word and
+  // the index of its first element in the row.
+  __device__ __forceinline__ void piece(int t, int& m, int& word, int& col) const {
+    m = t / per_row;
+    const int r = t - m * per_row, u = r / P, pc = r - u * P;
+    word = (m * P + pc) * stride + u;
+    col = (cu0 + u) * T::kUnitWeights + pc * 8;
+  }
+
+  // Sum of s[] over the workgroup, left in every thread (red: one float per
+  // wave and row).
+  __device__ __forceinline__ void block_sum(float (&s)[M], float (*red)[M]) const {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) {
+      const float v = group_sum(s[mm], 6);
+      if (lane == 0) red[wv][mm] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < THREADS / 64; ++w) v += red[w][mm];
+      s[mm] = v;
+    }
+  }
+
+  // torch.nn.LayerNorm over each row of the staged x, in place in LDS: mean
+  // and biased variance in fp32 (two passes), then
+  // fp16((x - mean) * rstd * weight + bias).
+  __device__ __forceinline__ void layer_norm(u32x4* xs) {
+    __shared__ float red1[THREADS / 64][M], red2[THREADS / 64][M];
+    const uint32_t ones = 0x3c003c00u;
+    float s[M], mean[M], rstd[M];
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) s[mm] = 0.f;
+    for (int t = threadIdx.x; t < total; t += THREADS) {
+      int m, word, col;
+      piece(t, m, word, col);
+      const u32x4 w = xs[word];
+      const float ps = dot2(w.w, ones, dot2(w.z, ones, dot2(w.y, ones, dot2(w.x, ones, 0.f))));
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) s[mm] += m == mm ? ps : 0.f;
+    }
+    block_sum(s, red1);
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) {
+      mean[mm] = s[mm] / (float)k;
+      s[mm] = 0.f;
+    }
+    for (int t = threadIdx.x; t < total; t += THREADS) {
+      int m, word, col;
+      piece(t, m, word, col);
+      float mu = mean[0];
+#pragma unroll
+      for (int mm = 1; mm < M; ++mm) mu = m == mm ? mean[mm] : mu;
+      const u32x4 w = xs[word];
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+      float q = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const h2_t h = __builtin_bit_cast(h2_t, ww[i]);
+        const float d0 = (float)h.x - mu, d1 = (float)h.y - mu;
+        q = fmaf(d0, d0, fmaf(d1, d1, q));
+      }
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) s[mm] += m == mm ? q : 0.f;
+    }
+    block_sum(s, red2);
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) rstd[mm] = 1.0f / sqrtf(s[mm] / (float)k + ln_eps);
+    for (int t = threadIdx.x; t < total; t += THREADS) {
+      int m, word, col;
+      piece(t, m, word, col);
+      float mu = mean[0], rs = rstd[0];
+#pragma unroll
+      for (int mm = 1; mm < M; ++mm) {
+        mu = m == mm ? mean[mm] : mu;
+        rs = m == mm ? rstd[mm] : rs;
+      }
+      const u32x4 w = xs[word];
+      const u32x4 g = ln_w ? *reinterpret_cast<const u32x4*>(ln_w + col)
+                           : u32x4{ones, ones, ones, ones};
+      const u32x4 b = ln_b ? *reinterpret_cast<const u32x4*>(ln_b + col) : u32x4{0, 0, 0, 0};
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, gg[4] = {g.x, g.y, g.z, g.w},
+                     bb[4] = {b.x, b.y, b.z, b.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const h2_t h = __builtin_bit_cast(h2_t, ww[i]);
+        const h2_t gh = __builtin_bit_cast(h2_t, gg[i]);
+        const h2_t bh = __builtin_bit_cast(h2_t, bb[i]);
+        h2_t r;
+        r.x = (_Float16)fmaf(((float)h.x - mu) * rs, (float)gh.x, (float)bh.x);
+        r.y = (_Float16)fmaf(((float)h.y - mu) * rs, (float)gh.y, (float)bh.y);
+        o[i] = __builtin_bit_cast(uint32_t, r);
+      }
+      xs[word] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+    __syncthreads();
+  }
+
   __device__ __forceinline__ void finish(u32x4* xs, float* sxs) {
     store_batch(xs);
     for (int base = threadIdx.x + SB * THREADS; base < total; base += SB * THREADS) {
@@ -370,6 +512,7 @@ struct XStager {
       store_batch(xs);
     }
     __syncthreads();
+    if (ln_w || ln_b) layer_norm(xs);
     const uint32_t ones = 0x3c003c00u;  // fp16 pair (1, 1)
     for (int t = threadIdx.x; t < M * cun; t += THREADS) {
       const int m = t / cun, u = t - m * cun;
@@ -397,30 +540,28 @@ __device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, int k,
   st.finish(xs, sxs);
 }
 
-// Sum of v over the G = 1 << lg_g consecutive lanes of a lane group, left in
-// every lane of the group: DPP quad permutes and row mirrors within 16 lanes,
-// then the gfx950 lane-swap instructions across 16- and 32-lane halves. No
-// LDS traffic.
-__device__ __forceinline__ float group_sum(float v, int lg_g) {
-  auto dpp = [](float f, auto ctrl) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
-        __builtin_bit_cast(int, f), decltype(ctrl)::value, 0xf, 0xf, false));
-  };
-  if (lg_g >= 1) v += dpp(v, std::integral_constant<int, 0xb1>{});   // quad_perm [1,0,3,2]
-  if (lg_g >= 2) v += dpp(v, std::integral_constant<int, 0x4e>{});   // quad_perm [2,3,0,1]
-  if (lg_g >= 3) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
-  if (lg_g >= 4) v += dpp(v, std::integral_constant<int, 0x140>{});  // row_mirror
-  if (lg_g >= 5) {
-    const int i = __builtin_bit_cast(int, v);
-    const auto r = __builtin_amdgcn_permlane16_swap(i, i, false, false);
-    v = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+// GELU with the tanh approximation (Hendrycks and Gimpel, 2016):
+// 0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3))), in fp32.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float kSqrt2OverPi = 0.7978845608028654f;
+  const float inner = kSqrt2OverPi * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// Store y[m, row] = v (the bias-added fp32 result) with the fused epilogue:
+// fp32 output as is; fp16 output rounded, then GELU (rounded again), then
+// the residual added (rounded again), each step as the separate fp16 torch op
+// it replaces.
+__device__ __forceinline__ void store_y(const GemvArgs& a, int m, int row, float v) {
+  const size_t i = (size_t)m * a.n + row;
+  if (a.y_f32) {
+    reinterpret_cast<float*>(a.y)[i] = v;
+    return;
   }
-  if (lg_g >= 6) {
-    const int i = __builtin_bit_cast(int, v);
-    const auto r = __builtin_amdgcn_permlane32_swap(i, i, false, false);
-    v = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
-  }
-  return v;
+  _Float16 t = (_Float16)v;
+  if (a.act == 1) t = (_Float16)gelu_tanh((float)t);
+  if (a.residual) t = (_Float16)(half_bits_to_float(a.residual[i]) + (float)t);
+  reinterpret_cast<_Float16*>(a.y)[i] = t;
 }
 
 }  // namespace svq

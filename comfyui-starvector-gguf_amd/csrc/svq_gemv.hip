@@ -181,10 +181,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const float v = __builtin_fmaf(acc[r][m], T::kOutScale, bias[r]);
-      if (a.y_f32)
-        reinterpret_cast<float*>(a.y)[(size_t)m * n + row] = v;
-      else
-        reinterpret_cast<_Float16*>(a.y)[(size_t)m * n + row] = (_Float16)v;
+      store_y(a, m, row, v);
     }
   }
 }

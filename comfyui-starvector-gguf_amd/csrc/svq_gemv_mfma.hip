@@ -368,10 +368,7 @@ __global__ __launch_bounds__(1024) void gemv_mfma_kernel(GemvArgs a) {
                 const int m = 4 * t + i;
                 if (m < M) {
                   const float v = __builtin_fmaf(acc[r][i], T::kOutScale, bsum);
-                  if (a.y_f32)
-                    reinterpret_cast<float*>(a.y)[(size_t)m * n + row] = v;
-                  else
-                    reinterpret_cast<_Float16*>(a.y)[(size_t)m * n + row] = (_Float16)v;
+                  store_y(a, m, row, v);
                 }
               }
             }

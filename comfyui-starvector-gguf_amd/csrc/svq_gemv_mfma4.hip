@@ -199,6 +199,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   for (int d = 0; d < D; ++d) issue(d);
   uint32_t bias_bits[R];
   load_bias(tile_of(0), bias_bits);
+  st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
   st.finish(xs, sxs);
 
   float acc[R][M];
@@ -292,10 +293,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 #pragma unroll
               for (int m = 0; m < M; ++m) {
                 const float v = __builtin_fmaf(acc[r][m], Mfma4Traits<QT>::kOutScale, b);
-                if (a.y_f32)
-                  reinterpret_cast<float*>(a.y)[(size_t)m * n + row] = v;
-                else
-                  reinterpret_cast<_Float16*>(a.y)[(size_t)m * n + row] = (_Float16)v;
+                store_y(a, m, row, v);
               }
             }
           }

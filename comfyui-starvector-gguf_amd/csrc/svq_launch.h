@@ -19,6 +19,12 @@ struct GemvArgs {
   int waves;        // streaming waves in the grid (streaming kernel)
   int slots;        // row tiles per workgroup (MFMA kernel)
   int ksplit;       // K splits per row tile (MFMA kernel)
+  // Fusions (streaming kernels only for the LayerNorm; fp16 y only):
+  const uint16_t* ln_w;      // LayerNorm of every x row before the product:
+  const uint16_t* ln_b;      //   fp16 [k] weight and bias (either may be nullptr)
+  float ln_eps;              //   (no LayerNorm when both are nullptr)
+  const uint16_t* residual;  // fp16 [m, n] added to the rounded output, or nullptr
+  int act;                   // 0 none, 1 tanh-approximated GELU of the rounded output
 };
 
 struct GemvShape {

@@ -8,8 +8,9 @@ runtime_shared.py (CachedDecoding :345-394) and its beam sampling
 + 1 times (q, k and v are one fused linear: their SoA rows concatenated, a pure
 byte concatenation). On the GPU a decode step's attention (rotation of q and
 k, the cache write and grouped-query attention over the cache) is one HIP
-kernel per layer (`svq_decode_attention`). Prefill attention, LayerNorm,
-sampling and host decoding use PyTorch ops.
+kernel per layer (`svq_decode_attention`), and the LayerNorms, GELU and
+residual adds run inside the GEMVs (`svq_gemv_fused`). Prefill, sampling and
+host decoding use PyTorch ops.
 
 Attention products are arranged so that no batched product takes a transposed
 view as its right operand: decode computes K @ q^T with a contiguous q^T, and
@@ -111,17 +112,21 @@ class Starcoder2Block(nn.Module):
         cfg = self.cfg
         hd, heads, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
         rows, length, hidden = x.shape
-        qkv = self.qkv_proj(self.input_layernorm(x))
         if position is not None and x.is_cuda:
-            # Rotation, cache write and attention in one HIP kernel.
+            # A decode step on the GPU: five HIP launches per layer. The
+            # LayerNorms, GELU and residual adds run inside the GEMVs; the
+            # rotation, cache write and attention are one kernel (+ merge).
+            x = x.reshape(rows, hidden)
+            qkv = fused_linear(self.qkv_proj, x, norm=self.input_layernorm)
             out = torch.empty((rows, hidden), dtype=x.dtype, device=x.device)
             workspace = native.attention_workspace(x.device, rows, heads, kvh, keys.shape[2])
-            native.decode_attention(qkv.view(rows, -1), cos.view(-1), sin.view(-1), keys,
-                                    values, position, bias, out, heads, kvh, hd ** -0.5,
-                                    workspace)
-            out = out.view(rows, 1, hidden)
-        else:
-            out = self.torch_attention(qkv, cos, sin, keys, values, position, bias)
+            native.decode_attention(qkv, cos.view(-1), sin.view(-1), keys, values, position,
+                                    bias, out, heads, kvh, hd ** -0.5, workspace)
+            x = fused_linear(self.o_proj, out, residual=x)
+            h = fused_linear(self.c_fc, x, norm=self.post_attention_layernorm, gelu=True)
+            return fused_linear(self.c_proj, h, residual=x).view(rows, 1, hidden)
+        qkv = self.qkv_proj(self.input_layernorm(x))
+        out = self.torch_attention(qkv, cos, sin, keys, values, position, bias)
         x = x + self.o_proj(out)
         return x + self.c_proj(F.gelu(self.c_fc(self.post_attention_layernorm(x)), approximate="tanh"))
 
@@ -149,6 +154,24 @@ class Starcoder2Block(nn.Module):
         scores = torch.bmm(kb, qt).transpose(1, 2) * hd ** -0.5 + bias
         probs = torch.softmax(scores, -1, dtype=torch.float32).to(qkv.dtype).contiguous()
         return torch.bmm(probs, values.flatten(0, 1)).view(rows, 1, hidden)
+
+
+def fused_linear(linear, x, norm=None, residual=None, gelu=False):
+    """`linear` (a GGUFLinear) on fp16 rows x [m, k] with the ops around it in
+    one `svq_gemv_fused` launch: residual + gelu(linear(norm(x))), each part
+    optional, rounded to fp16 after every op as the separate torch ops are."""
+    spec = linear._specs["weight"]
+    n, k = spec.shape
+    if x.shape[-1] != k or x.dim() != 2:
+        raise ValueError(f"expected [m, {k}] rows, got {tuple(x.shape)}")
+    y = torch.empty((x.shape[0], n), dtype=torch.float16, device=x.device)
+    native.gemv_fused(x.contiguous(), linear.weight, linear.weight_scales.view(torch.float16), y,
+                      spec.qtype, bias=linear.unpack("bias", torch.float16, x.device),
+                      ln_weight=None if norm is None else norm.weight,
+                      ln_bias=None if norm is None else norm.bias,
+                      ln_eps=1e-5 if norm is None else norm.eps, residual=residual,
+                      activation="gelu_tanh" if gelu else None)
+    return y
 
 
 def causal_attention(q, k, v, group):
@@ -230,6 +253,8 @@ class Starcoder2Decoder(nn.Module):
         x = self.embed_tokens(tokens)[:, None]
         for layer, lk, lv in zip(self.layers, keys, values):
             x = layer(x, cos, sin, lk[:, :, :span], lv[:, :, :span], position, bias)
+        if x.is_cuda:
+            return fused_linear(self.lm_head, x[:, 0], norm=self.norm)
         return self.lm_head(self.norm(x[:, 0]))
 
 

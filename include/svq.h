@@ -57,6 +57,10 @@ extern "C" {
                               (q: 4 bytes for Q5_0; s, bias: 2 bytes) */
 #define SVQ_E_WORKSPACE (-7) /* workspace smaller than the call needs */
 
+/* Activations of svq_gemv_fused. */
+#define SVQ_ACT_NONE 0
+#define SVQ_ACT_GELU_TANH 1 /* F.gelu(..., approximate='tanh') */
+
 #define SVQ_HEAD_DIM 128 /* head dimension of svq_decode_attention */
 #define SVQ_MAX_GROUP 16 /* largest query heads per key/value head */
 
@@ -83,6 +87,30 @@ const char *svq_last_error(void);
 int svq_gemv(const void *x, const uint8_t *q, const uint16_t *s,
              const uint16_t *bias, void *y, int m, int n, int k, int qtype,
              int y_dtype, void *stream);
+
+/*
+ * svq_gemv with the decoder-layer ops around it fused in; y is fp16:
+ *   y = residual + act(fp16(W . fp16(LayerNorm(x)) + bias))
+ * Replaces the op sequences around the reference's quantized linears in a
+ * decode step (runtime_8b.py:37, 53-54 and 110; runtime_1b.py:33, 46-47 and
+ * 91): `input_layernorm` / `post_attention_layernorm` / `norm` before
+ * `q/k/v_proj`, `c_fc` and `lm_head`, `F.gelu(approximate='tanh')` after
+ * `c_fc`, and the residual `x + o_proj(...)`, `x + c_proj(...)`.
+ *   ln_weight, ln_bias  fp16 [k] (16-byte aligned), or both NULL for no
+ *             LayerNorm; ln_eps as torch.nn.LayerNorm's eps. Each x row is
+ *             normalized with fp32 statistics and rounded to fp16 before the
+ *             product, as the separate LayerNorm's fp16 output.
+ *   activation  SVQ_ACT_NONE or SVQ_ACT_GELU_TANH, applied to the rounded
+ *             product and rounded again
+ *   residual  fp16 [m, n] added last (then rounded), or NULL; may be y itself
+ *             (in place); y must not alias x.
+ * With a LayerNorm, x must fit the streaming kernels' LDS staging (m * k * 2
+ * bytes plus offset sums within 156 KB), otherwise SVQ_E_SHAPE.
+ */
+int svq_gemv_fused(const void *x, const uint8_t *q, const uint16_t *s,
+                   const uint16_t *bias, void *y, int m, int n, int k, int qtype,
+                   const uint16_t *ln_weight, const uint16_t *ln_bias, float ln_eps,
+                   const uint16_t *residual, int activation, void *stream);
 
 /*
  * Diagnostic with no counterpart in the reference (whose launch tuple is the

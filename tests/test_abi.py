@@ -23,7 +23,7 @@ def declared_functions():
 def test_header_declares_the_entry_points():
     names = declared_functions()
     assert {"svq_abi_version", "svq_last_error", "svq_gemv", "svq_dequant",
-            "svq_dequant_rows", "svq_decode_attention",
+            "svq_dequant_rows", "svq_decode_attention", "svq_gemv_fused",
             "svq_decode_attention_workspace"} <= set(names)
 
 
@@ -147,3 +147,26 @@ def test_decode_attention_workspace_size():
     assert lib.svq_decode_attention_workspace(2, 16, 1, 64) == 256 + 2 * 16 * 512
     assert lib.svq_decode_attention_workspace(2, 36, 5, 64) == -2
     assert lib.svq_decode_attention_workspace(2, 34, 2, 64) == -2  # 17 heads per kv head
+
+
+def gemv_fused(**kw):
+    args = dict(x=FAKE, q=FAKE, s=FAKE, bias=None, y=FAKE + 1024, m=2, n=8, k=64, qtype=4,
+                ln_w=None, ln_b=None, eps=1e-5, res=None, act=0)
+    args.update(kw)
+    return native.load().svq_gemv_fused(
+        args["x"], args["q"], args["s"], args["bias"], args["y"], args["m"], args["n"],
+        args["k"], args["qtype"], args["ln_w"], args["ln_b"], args["eps"], args["res"],
+        args["act"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(act=2), -4), (dict(ln_w=FAKE + 2), -6), (dict(ln_b=FAKE + 8), -6),
+    (dict(res=FAKE + 1), -6), (dict(ln_w=FAKE, eps=-1.0), -2),
+    (dict(y=FAKE, res=FAKE + 64), -2),
+    (dict(qtype=3), -1), (dict(m=9), -2), (dict(k=40), -2), (dict(x=None), -3),
+    # x of 8 rows x 18432 does not fit the LDS staging the LayerNorm needs
+    (dict(m=8, k=18432, n=64, ln_w=FAKE), -2),
+])
+def test_gemv_fused_rejects_bad_arguments(kw, code):
+    assert gemv_fused(**kw) == code
+    assert native.load().svq_last_error().decode()
