@@ -149,9 +149,9 @@ constexpr size_t kStreamLdsMax = 156 * 1024;  // nearly all of a CU's 160 KB
 // exceeds the 2^31-byte ranges the kernel addresses.
 bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out,
                    int* rows_out, int* wpg_out, int* waves_out, int* groups_out,
-                   int* wmax_out = nullptr) {
+                   int* wmax_out = nullptr, size_t extra_lds = 0) {
   if (tu.path == 2) return false;
-  const size_t lds = svq::stream_lds_bytes(qtype, m, k);
+  const size_t lds = svq::stream_lds_bytes(qtype, m, k) + extra_lds;
   const uint64_t q_bytes = (uint64_t)n * (k / 32) * payload_bytes(qtype);
   if (lds > kStreamLdsMax || q_bytes >= (1ull << 31) || (uint64_t)n * (k / 16) >= (1ull << 31))
     return false;
@@ -167,7 +167,7 @@ bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out
   while (lg_cap < 6 && (units >> (lg_cap + 1)) >= 4) ++lg_cap;
   int lg = lg0, rows = 2, wmax = 0, tiles = 0;
   for (;;) {
-    wmax = cus * waves_per_cu(dev, svq::stream_kernel(qtype, m, rows, wpg), wpg, lds);
+    wmax = cus * waves_per_cu(dev, svq::stream_kernel(qtype, m, rows, wpg, extra_lds > 0), wpg, lds);
     tiles = (n + ((64 >> lg) * rows) - 1) / ((64 >> lg) * rows);
     if (tiles >= wmax) break;
     if (rows == 2) rows = 1;
@@ -177,7 +177,7 @@ bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out
   if (tu.lg_g >= 0) lg = tu.lg_g;
   if (tu.rows) rows = tu.rows;
   if (tu.lg_g >= 0 || tu.rows) {
-    wmax = cus * waves_per_cu(dev, svq::stream_kernel(qtype, m, rows, wpg), wpg, lds);
+    wmax = cus * waves_per_cu(dev, svq::stream_kernel(qtype, m, rows, wpg, extra_lds > 0), wpg, lds);
     tiles = (n + ((64 >> lg) * rows) - 1) / ((64 >> lg) * rows);
   }
   int waves = tiles < wmax ? tiles : wmax;
@@ -204,7 +204,7 @@ constexpr int kMfmaMinRows = 5;  // smallest M sent to the MFMA kernel by defaul
 // persistent over tile groups, trimmed so that each processes the same number
 // of groups.
 bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_out,
-                  int* ksplit_out, int* groups_out, int* wmax_out) {
+                  int* ksplit_out, int* groups_out, int* wmax_out, size_t extra_lds = 0) {
   if ((tu.path != 4 && tu.path != 0) || m > 4) return false;
   // Automatic choice (measured at the StarCoder2-8B and GPTBigCode-1B shapes):
   // the matrix-core path wins for Q5_0 at every M and for Q4_0 / Q8_0 from
@@ -223,9 +223,9 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   int wmax = 0, tiles = 0;
   size_t lds = 0;
   for (;;) {
-    lds = svq::mfma4_lds_bytes(qtype, m, k, rows, 4);
+    lds = svq::mfma4_lds_bytes(qtype, m, k, rows, 4) + extra_lds;
     if (lds > kStreamLdsMax) return false;
-    wmax = cus * waves_per_cu(dev, svq::mfma4_kernel(qtype, m, rows), wpg, lds);
+    wmax = cus * waves_per_cu(dev, svq::mfma4_kernel(qtype, m, rows, extra_lds > 0), wpg, lds);
     const int tile_rows = rows == 2 ? 8 : 4;
     tiles = (n + tile_rows - 1) / tile_rows;
     if (tiles >= wmax || rows != 2 || tu.mfma_r) break;
@@ -356,7 +356,8 @@ int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t
   hipError_t e;
   int wmax = 0;
   // The LayerNorm runs in the x staging of the two streaming kernels.
-  if (choose_mfma4(m, n, k, qtype, tu, &rows, &ksplit, &groups, &wmax)) {
+  const size_t ln_lds = svq::layer_norm_lds_bytes(k, f.layer_norm());
+  if (choose_mfma4(m, n, k, qtype, tu, &rows, &ksplit, &groups, &wmax, ln_lds)) {
     a.ksplit = ksplit;
     e = svq::launch_gemv_mfma4(a, qtype, m, rows, groups, static_cast<hipStream_t>(stream));
   } else if (!f.layer_norm() &&
@@ -365,7 +366,7 @@ int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t
     a.ksplit = ksplit;
     e = svq::launch_gemv_mfma(a, qtype, m, rows, groups, static_cast<hipStream_t>(stream));
   } else if (choose_stream(m, n, k, qtype, f.layer_norm() ? Tuning{} : tu, &lg, &rows, &wpg,
-                           &waves, &groups)) {
+                           &waves, &groups, nullptr, ln_lds)) {
     a.lg_g = lg;
     a.waves = waves;
     e = svq::launch_gemv_stream(a, qtype, m, rows, wpg, groups,

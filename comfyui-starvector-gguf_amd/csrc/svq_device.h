@@ -358,7 +358,7 @@ __device__ __forceinline__ float group_sum(float v, int lg_g) {
 // consumed on every path.
 // SxMul multiplies the offset term: 16 for a kernel that places every Q4_0
 // code as 16 * code (both nibble halves scaled alike).
-template <int QT, int M, int THREADS, int SB, int SxMul = 1>
+template <int QT, int M, int THREADS, int SB, int SxMul = 1, bool LN = false>
 struct XStager {
   using T = QTraits<QT>;
   static constexpr int P = T::kUnitWeights / 8;
@@ -389,9 +389,17 @@ struct XStager {
     for (int j = 0; j < SB; ++j) xs[dst[j]] = v[j];
   }
 
-  __device__ __forceinline__ void begin() { load_batch(threadIdx.x); }
-
-  // LayerNorm of every staged row (full rows only: cu0 == 0, cun units = k).
+  // LayerNorm of every staged row (LN kernels only; full rows only: cu0 == 0,
+  // cun units = k). Its weight and bias pieces (8 columns each) are copied to LDS by the
+  // buffer unit (loads with an LDS destination, no registers) in begin(),
+  // before the x loads: wave w copies the 64-piece blocks w, w + W, ...
+  // (W waves) of each array to lns[block * 64 ...] (weight) and
+  // lns[ln_cols() + block * 64 ...] (bias). Vector loads retire in issue
+  // order, so the wait for a wave's own x pieces in finish() also covers its
+  // copies, and the barrier after the x stores makes every copy visible
+  // before the normalization reads them; no wait on the loads a kernel issues
+  // between begin() and finish() is involved.
+  static constexpr int kWaves = THREADS / 64;
   const uint16_t* ln_w = nullptr;
   const uint16_t* ln_b = nullptr;
   float ln_eps = 0.f;
@@ -401,14 +409,27 @@ struct XStager {
     ln_b = b;
     ln_eps = eps;
   }
+  __device__ __forceinline__ bool has_layer_norm() const { return ln_w || ln_b; }
+  // Pieces per parameter array in LDS: k / 8 rounded up to whole 64-piece
+  // blocks (the copy writes 64 pieces per instruction).
+  __device__ __forceinline__ int ln_cols() const { return (k / 8 + 63) / 64 * 64; }
 
-  // Piece t of the staged rows in row-major order: its row, its LDS word and
-  // the index of its first element in the row.
-  __device__ __forceinline__ void piece(int t, int& m, int& word, int& col) const {
-    m = t / per_row;
-    const int r = t - m * per_row, u = r / P, pc = r - u * P;
-    word = (m * P + pc) * stride + u;
-    col = (cu0 + u) * T::kUnitWeights + pc * 8;
+  __device__ __forceinline__ void begin(u32x4* lns = nullptr) {
+    if (LN && has_layer_norm()) {
+      const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, cols = k / 8;
+      // A missing array is a zero-length range: its copy writes zeros.
+      const __amdgpu_buffer_rsrc_t wr = make_rsrc(ln_w, ln_w ? (uint32_t)cols * 16u : 0u);
+      const __amdgpu_buffer_rsrc_t br = make_rsrc(ln_b, ln_b ? (uint32_t)cols * 16u : 0u);
+      for (int blk = wv; blk * 64 < cols; blk += kWaves) {
+        const uint32_t off = (uint32_t)(blk * 64 + lane) * 16u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            wr, (__attribute__((address_space(3))) void*)(lns + blk * 64), 16, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            br, (__attribute__((address_space(3))) void*)(lns + ln_cols() + blk * 64), 16, off,
+            0, 0, 0);
+      }
+    }
+    load_batch(threadIdx.x);
   }
 
   // Sum of s[] over the workgroup, left in every thread (red: one float per
@@ -432,20 +453,101 @@ struct XStager {
 
   // torch.nn.LayerNorm over each row of the staged x, in place in LDS: mean
   // and biased variance in fp32 (two passes), then
-  // fp16((x - mean) * rstd * weight + bias).
-  __device__ __forceinline__ void layer_norm(u32x4* xs) {
+  // fp16((x - mean) * rstd * weight + bias). Piece (m, pc, u) of the LDS
+  // layout holds columns u * kUnitWeights + pc * 8 .. + 7 of row m.
+  __device__ __forceinline__ void layer_norm(u32x4* xs, const u32x4* lns) {
     __shared__ float red1[THREADS / 64][M], red2[THREADS / 64][M];
     const uint32_t ones = 0x3c003c00u;
     float s[M], mean[M], rstd[M];
 #pragma unroll
+    for (int mm = 0; mm < M; ++mm) {
+      s[mm] = 0.f;
+#pragma unroll
+      for (int pc = 0; pc < P; ++pc)
+        for (int u = threadIdx.x; u < cun; u += THREADS) {
+          const u32x4 w = xs[(mm * P + pc) * stride + u];
+          s[mm] = dot2(w.w, ones, dot2(w.z, ones, dot2(w.y, ones, dot2(w.x, ones, s[mm]))));
+        }
+    }
+    block_sum(s, red1);
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) {
+      mean[mm] = s[mm] / (float)k;
+      float q = 0.f;
+#pragma unroll
+      for (int pc = 0; pc < P; ++pc)
+        for (int u = threadIdx.x; u < cun; u += THREADS) {
+          const u32x4 w = xs[(mm * P + pc) * stride + u];
+          const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const h2_t h = __builtin_bit_cast(h2_t, ww[i]);
+            const float d0 = (float)h.x - mean[mm], d1 = (float)h.y - mean[mm];
+            q = fmaf(d0, d0, fmaf(d1, d1, q));
+          }
+        }
+      s[mm] = q;
+    }
+    block_sum(s, red2);
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm) rstd[mm] = 1.0f / sqrtf(s[mm] / (float)k + ln_eps);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, cols = k / 8, bcol = ln_cols();
+    const bool unit_w = ln_w == nullptr;
+    for (int blk = wv; blk * 64 < cols; blk += kWaves) {
+      const int c = blk * 64 + lane;
+      if (c >= cols) continue;
+      const int u = c / P, pc = c - u * P;
+      const u32x4 g = lns[c], b = lns[bcol + c];
+      const uint32_t gg[4] = {g.x, g.y, g.z, g.w}, bb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int mm = 0; mm < M; ++mm) {
+        const int word = (mm * P + pc) * stride + u;
+        const u32x4 w = xs[word];
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const h2_t h = __builtin_bit_cast(h2_t, ww[i]);
+          const h2_t gh = __builtin_bit_cast(h2_t, gg[i]);
+          const h2_t bh = __builtin_bit_cast(h2_t, bb[i]);
+          const float g0 = unit_w ? 1.0f : (float)gh.x, g1 = unit_w ? 1.0f : (float)gh.y;
+          h2_t r;
+          r.x = (_Float16)fmaf(((float)h.x - mean[mm]) * rstd[mm], g0, (float)bh.x);
+          r.y = (_Float16)fmaf(((float)h.y - mean[mm]) * rstd[mm], g1, (float)bh.y);
+          o[i] = __builtin_bit_cast(uint32_t, r);
+        }
+        xs[word] = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+    __syncthreads();
+  }
+
+  // The LayerNorm when the first batch holds every piece of x (total <=
+  // SB * THREADS): statistics from the registers, then only the normalized
+  // pieces are written to LDS. Two barriers fewer than layer_norm().
+  __device__ __forceinline__ void layer_norm_registers(u32x4* xs, const u32x4* lns) {
+    __shared__ float red1[THREADS / 64][M], red2[THREADS / 64][M];
+    const uint32_t ones = 0x3c003c00u;
+    int row[SB], col[SB];
+    bool valid[SB];
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int t = threadIdx.x + j * THREADS;
+      valid[j] = t < total;
+      int m = 0, r = valid[j] ? t : 0;
+      while (r >= per_row) { r -= per_row; ++m; }
+      row[j] = m;
+      col[j] = r;  // = u * P + pc: the piece's column / 8 (full rows)
+    }
+    float s[M], mean[M], rstd[M];
+#pragma unroll
     for (int mm = 0; mm < M; ++mm) s[mm] = 0.f;
-    for (int t = threadIdx.x; t < total; t += THREADS) {
-      int m, word, col;
-      piece(t, m, word, col);
-      const u32x4 w = xs[word];
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const u32x4 w = v[j];
       const float ps = dot2(w.w, ones, dot2(w.z, ones, dot2(w.y, ones, dot2(w.x, ones, 0.f))));
 #pragma unroll
-      for (int mm = 0; mm < M; ++mm) s[mm] += m == mm ? ps : 0.f;
+      for (int mm = 0; mm < M; ++mm) s[mm] += valid[j] && row[j] == mm ? ps : 0.f;
     }
     block_sum(s, red1);
 #pragma unroll
@@ -453,14 +555,12 @@ struct XStager {
       mean[mm] = s[mm] / (float)k;
       s[mm] = 0.f;
     }
-    for (int t = threadIdx.x; t < total; t += THREADS) {
-      int m, word, col;
-      piece(t, m, word, col);
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
       float mu = mean[0];
 #pragma unroll
-      for (int mm = 1; mm < M; ++mm) mu = m == mm ? mean[mm] : mu;
-      const u32x4 w = xs[word];
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+      for (int mm = 1; mm < M; ++mm) mu = row[j] == mm ? mean[mm] : mu;
+      const uint32_t ww[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
       float q = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -469,25 +569,24 @@ struct XStager {
         q = fmaf(d0, d0, fmaf(d1, d1, q));
       }
 #pragma unroll
-      for (int mm = 0; mm < M; ++mm) s[mm] += m == mm ? q : 0.f;
+      for (int mm = 0; mm < M; ++mm) s[mm] += valid[j] && row[j] == mm ? q : 0.f;
     }
     block_sum(s, red2);
 #pragma unroll
     for (int mm = 0; mm < M; ++mm) rstd[mm] = 1.0f / sqrtf(s[mm] / (float)k + ln_eps);
-    for (int t = threadIdx.x; t < total; t += THREADS) {
-      int m, word, col;
-      piece(t, m, word, col);
+    const int bcol = ln_cols();
+    const bool unit_w = ln_w == nullptr;
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      if (!valid[j]) continue;
       float mu = mean[0], rs = rstd[0];
 #pragma unroll
       for (int mm = 1; mm < M; ++mm) {
-        mu = m == mm ? mean[mm] : mu;
-        rs = m == mm ? rstd[mm] : rs;
+        mu = row[j] == mm ? mean[mm] : mu;
+        rs = row[j] == mm ? rstd[mm] : rs;
       }
-      const u32x4 w = xs[word];
-      const u32x4 g = ln_w ? *reinterpret_cast<const u32x4*>(ln_w + col)
-                           : u32x4{ones, ones, ones, ones};
-      const u32x4 b = ln_b ? *reinterpret_cast<const u32x4*>(ln_b + col) : u32x4{0, 0, 0, 0};
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, gg[4] = {g.x, g.y, g.z, g.w},
+      const u32x4 g = lns[col[j]], b = lns[bcol + col[j]];
+      const uint32_t ww[4] = {v[j].x, v[j].y, v[j].z, v[j].w}, gg[4] = {g.x, g.y, g.z, g.w},
                      bb[4] = {b.x, b.y, b.z, b.w};
       uint32_t o[4];
 #pragma unroll
@@ -495,24 +594,31 @@ struct XStager {
         const h2_t h = __builtin_bit_cast(h2_t, ww[i]);
         const h2_t gh = __builtin_bit_cast(h2_t, gg[i]);
         const h2_t bh = __builtin_bit_cast(h2_t, bb[i]);
+        const float g0 = unit_w ? 1.0f : (float)gh.x, g1 = unit_w ? 1.0f : (float)gh.y;
         h2_t r;
-        r.x = (_Float16)fmaf(((float)h.x - mu) * rs, (float)gh.x, (float)bh.x);
-        r.y = (_Float16)fmaf(((float)h.y - mu) * rs, (float)gh.y, (float)bh.y);
+        r.x = (_Float16)fmaf(((float)h.x - mu) * rs, g0, (float)bh.x);
+        r.y = (_Float16)fmaf(((float)h.y - mu) * rs, g1, (float)bh.y);
         o[i] = __builtin_bit_cast(uint32_t, r);
       }
-      xs[word] = u32x4{o[0], o[1], o[2], o[3]};
+      xs[dst[j]] = u32x4{o[0], o[1], o[2], o[3]};
     }
     __syncthreads();
   }
 
-  __device__ __forceinline__ void finish(u32x4* xs, float* sxs) {
-    store_batch(xs);
-    for (int base = threadIdx.x + SB * THREADS; base < total; base += SB * THREADS) {
-      load_batch(base);
+  // lns: the LDS that begin() filled with the LayerNorm parameters
+  // (2 * ln_cols() pieces), used only when set_layer_norm() gave any.
+  __device__ __forceinline__ void finish(u32x4* xs, float* sxs, u32x4* lns = nullptr) {
+    if (LN && has_layer_norm() && total <= SB * THREADS) {
+      layer_norm_registers(xs, lns);
+    } else {
       store_batch(xs);
+      for (int base = threadIdx.x + SB * THREADS; base < total; base += SB * THREADS) {
+        load_batch(base);
+        store_batch(xs);
+      }
+      __syncthreads();
+      if (LN && has_layer_norm()) layer_norm(xs, lns);
     }
-    __syncthreads();
-    if (ln_w || ln_b) layer_norm(xs);
     const uint32_t ones = 0x3c003c00u;  // fp16 pair (1, 1)
     for (int t = threadIdx.x; t < M * cun; t += THREADS) {
       const int m = t / cun, u = t - m * cun;

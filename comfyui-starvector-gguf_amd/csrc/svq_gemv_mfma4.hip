@@ -81,7 +81,7 @@ __device__ __forceinline__ float slot_sum(float v) {
 // 60 bytes as three 16-byte loads and one 12-byte load and its three scales as
 // 2 + 4 bytes: 6 loads per 3 units instead of 9, which the memory pipeline
 // serves about 13% faster. It needs units % 48 == 0 (K = 4608, 18432, ...).
-template <int QT, int M, int R, int D, int WPG, int U>
+template <int QT, int M, int R, int D, int WPG, int U, bool LN>
 __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   static_assert(M >= 1 && M <= 4, "A has 4 rows");
   static_assert(U == 1 || (U == 3 && QT == 5), "three units per lane: Q5_0 only");
@@ -122,8 +122,11 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 
   if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
   constexpr int XP = T::kUnitWeights / 8;  // 16-byte x pieces per unit
+  // LDS: x pieces, LayerNorm parameters (if any), offset sums, split-K sums.
+  const bool ln = LN && (a.ln_w || a.ln_b);
   u32x4* xs = lds;
-  float* sxs = reinterpret_cast<float*>(xs + M * XP * units);
+  u32x4* lns = xs + M * XP * units;
+  float* sxs = reinterpret_cast<float*>(lns + (ln ? 2 * ((k / 8 + 63) / 64 * 64) : 0));
   float* part = sxs + M * units;  // [2][WPG][R][M][4] split-K partial sums
 
   // Row offsets of this lane's R rows in tile `tile` (rows past n: out of
@@ -192,15 +195,15 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 
   // x loads first, then the weight prologue, then x is written to LDS
   // (vector loads retire in issue order).
-  XStager<QT, M, WPG * 64, kStage4Batch<QT, M>, Mfma4Traits<QT>::kSxMul> st(a.x, k, 0, units,
-                                                                           units);
-  st.begin();
+  XStager<QT, M, WPG * 64, kStage4Batch<QT, M>, Mfma4Traits<QT>::kSxMul, LN> st(a.x, k, 0, units,
+                                                                               units);
+  st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
+  st.begin(lns);
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d);
   uint32_t bias_bits[R];
   load_bias(tile_of(0), bias_bits);
-  st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
-  st.finish(xs, sxs);
+  st.finish(xs, sxs, lns);
 
   float acc[R][M];
 #pragma unroll
@@ -310,66 +313,71 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   }
 }
 
-template <int QT, int M, int R, int D, int U>
+template <int QT, int M, int R, int D, int U, bool LN>
 const void* mfma4_kernel_ptr() {
-  return reinterpret_cast<const void*>(&gemv_mfma4_kernel<QT, M, R, D, kStreamWavesPerGroup, U>);
+  return reinterpret_cast<const void*>(&gemv_mfma4_kernel<QT, M, R, D, kStreamWavesPerGroup, U, LN>);
 }
 
-template <int QT, int M, int R, int D, int U>
+template <int QT, int M, int R, int D, int U, bool LN>
 hipError_t mfma4_launch(const GemvArgs& a, int groups, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((gemv_mfma4_kernel<QT, M, R, D, kStreamWavesPerGroup, U>), dim3(groups),
+  hipLaunchKernelGGL((gemv_mfma4_kernel<QT, M, R, D, kStreamWavesPerGroup, U, LN>), dim3(groups),
                      dim3(kStreamWavesPerGroup * 64), lds, stream, a);
   return hipGetLastError();
+}
+
+// One (R, D, U) variant, with or without the LayerNorm staging.
+template <int QT, int M, int R, int D, int U>
+hipError_t mfma4_variant(const GemvArgs& a, bool ln, int groups, size_t lds, hipStream_t stream,
+                         const void** fn) {
+  if (fn) {
+    *fn = ln ? mfma4_kernel_ptr<QT, M, R, D, U, true>() : mfma4_kernel_ptr<QT, M, R, D, U, false>();
+    return hipSuccess;
+  }
+  return ln ? mfma4_launch<QT, M, R, D, U, true>(a, groups, lds, stream)
+            : mfma4_launch<QT, M, R, D, U, false>(a, groups, lds, stream);
 }
 
 // rows 1: one row set per lane with an 8-deep ring; rows 2: two row sets
 // (sharing each x read) with a 4-deep ring; rows 3 (Q5_0): one row set, three
 // consecutive units per lane, a 3-deep ring (9 units in flight).
 template <int QT, int M>
-hipError_t mfma4_dispatch_r(const GemvArgs& a, int rows, int groups, size_t lds,
+hipError_t mfma4_dispatch_r(const GemvArgs& a, bool ln, int rows, int groups, size_t lds,
                             hipStream_t stream, const void** fn) {
   if constexpr (QT == 5) {
-    if (rows == 3) {
-      if (fn) { *fn = mfma4_kernel_ptr<QT, M, 1, 3, 3>(); return hipSuccess; }
-      return mfma4_launch<QT, M, 1, 3, 3>(a, groups, lds, stream);
-    }
+    if (rows == 3) return mfma4_variant<QT, M, 1, 3, 3>(a, ln, groups, lds, stream, fn);
   }
-  if (rows == 2) {
-    if (fn) { *fn = mfma4_kernel_ptr<QT, M, 2, 4, 1>(); return hipSuccess; }
-    return mfma4_launch<QT, M, 2, 4, 1>(a, groups, lds, stream);
-  }
-  if (fn) { *fn = mfma4_kernel_ptr<QT, M, 1, 8, 1>(); return hipSuccess; }
-  return mfma4_launch<QT, M, 1, 8, 1>(a, groups, lds, stream);
+  if (rows == 2) return mfma4_variant<QT, M, 2, 4, 1>(a, ln, groups, lds, stream, fn);
+  return mfma4_variant<QT, M, 1, 8, 1>(a, ln, groups, lds, stream, fn);
 }
 
 template <int QT>
-hipError_t mfma4_dispatch_m(const GemvArgs& a, int m, int rows, int groups, size_t lds,
+hipError_t mfma4_dispatch_m(const GemvArgs& a, bool ln, int m, int rows, int groups, size_t lds,
                             hipStream_t stream, const void** fn) {
   switch (m) {
-    case 1: return mfma4_dispatch_r<QT, 1>(a, rows, groups, lds, stream, fn);
-    case 2: return mfma4_dispatch_r<QT, 2>(a, rows, groups, lds, stream, fn);
-    case 3: return mfma4_dispatch_r<QT, 3>(a, rows, groups, lds, stream, fn);
-    case 4: return mfma4_dispatch_r<QT, 4>(a, rows, groups, lds, stream, fn);
+    case 1: return mfma4_dispatch_r<QT, 1>(a, ln, rows, groups, lds, stream, fn);
+    case 2: return mfma4_dispatch_r<QT, 2>(a, ln, rows, groups, lds, stream, fn);
+    case 3: return mfma4_dispatch_r<QT, 3>(a, ln, rows, groups, lds, stream, fn);
+    case 4: return mfma4_dispatch_r<QT, 4>(a, ln, rows, groups, lds, stream, fn);
   }
   return hipErrorInvalidValue;
 }
 
-hipError_t mfma4_dispatch(const GemvArgs& a, int qtype, int m, int rows, int groups, size_t lds,
-                          hipStream_t stream, const void** fn) {
+hipError_t mfma4_dispatch(const GemvArgs& a, bool ln, int qtype, int m, int rows, int groups,
+                          size_t lds, hipStream_t stream, const void** fn) {
   switch (qtype) {
-    case 4: return mfma4_dispatch_m<4>(a, m, rows, groups, lds, stream, fn);
-    case 5: return mfma4_dispatch_m<5>(a, m, rows, groups, lds, stream, fn);
-    case 8: return mfma4_dispatch_m<8>(a, m, rows, groups, lds, stream, fn);
+    case 4: return mfma4_dispatch_m<4>(a, ln, m, rows, groups, lds, stream, fn);
+    case 5: return mfma4_dispatch_m<5>(a, ln, m, rows, groups, lds, stream, fn);
+    case 8: return mfma4_dispatch_m<8>(a, ln, m, rows, groups, lds, stream, fn);
   }
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-const void* mfma4_kernel(int qtype, int m, int rows) {
+const void* mfma4_kernel(int qtype, int m, int rows, bool ln) {
   const void* fn = nullptr;
   GemvArgs unused{};
-  (void)mfma4_dispatch(unused, qtype, m, rows, 0, 0, nullptr, &fn);
+  (void)mfma4_dispatch(unused, ln, qtype, m, rows, 0, 0, nullptr, &fn);
   return fn;
 }
 
@@ -381,7 +389,9 @@ size_t mfma4_lds_bytes(int qtype, int m, int k, int rows, int ksplit) {
 
 hipError_t launch_gemv_mfma4(const GemvArgs& a, int qtype, int m, int rows, int groups,
                              hipStream_t stream) {
-  return mfma4_dispatch(a, qtype, m, rows, groups, mfma4_lds_bytes(qtype, m, a.k, rows, a.ksplit),
+  return mfma4_dispatch(a, a.ln_w || a.ln_b, qtype, m, rows, groups,
+                        mfma4_lds_bytes(qtype, m, a.k, rows, a.ksplit) +
+                            layer_norm_lds_bytes(a.k, a.ln_w || a.ln_b),
                         stream, nullptr);
 }
 

@@ -39,7 +39,7 @@ constexpr int kStageBatch =
     M <= 2 ? M * 144 * (QTraits<QT>::kUnitWeights / 8) * QTraits<QT>::kUnitsPerBlock / 256 + 1
            : 4;
 
-template <int QT, int M, int R, int D, int WPG>
+template <int QT, int M, int R, int D, int WPG, bool LN>
 __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   using T = QTraits<QT>;
   constexpr int P = T::kUnitWeights / 8;   // 16-byte activation pieces per unit
@@ -74,8 +74,11 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   // need no base register). Dynamic LDS: x pieces, then offset sums.
   __shared__ u32x2 q5_table[QT == 5 ? 256 : 1];
   if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
+  // LDS: x pieces, LayerNorm parameters (if any), offset sums.
+  const bool ln = LN && (a.ln_w || a.ln_b);
   u32x4* xs = lds;
-  float* sxs = reinterpret_cast<float*>(xs + M * P * units);
+  u32x4* lns = xs + M * P * units;
+  float* sxs = reinterpret_cast<float*>(lns + (ln ? 2 * ((k / 8 + 63) / 64 * 64) : 0));
 
   // Row byte offsets of this lane's R rows in tile `tile` (clamped to n - 1:
   // loaded, never stored).
@@ -127,14 +130,14 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   // cache round trip earlier than if x were staged completely first. (x loads
   // issued behind the prologue would wait for the whole chip-wide prologue
   // burst.) Pieces beyond the first batch are staged after the prologue.
-  XStager<QT, M, WPG * 64, kStageBatch<QT, M>> st(a.x, k, 0, units, units);
-  st.begin();
+  XStager<QT, M, WPG * 64, kStageBatch<QT, M>, 1, LN> st(a.x, k, 0, units, units);
+  st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
+  st.begin(lns);
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d);
   uint32_t bias_bits[R];
   load_bias(wid, bias_bits);
-  st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
-  st.finish(xs, sxs);
+  st.finish(xs, sxs, lns);
 
   float acc[R][M];
 #pragma unroll
@@ -208,60 +211,69 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   }
 }
 
-template <int QT, int M, int R, int D, int WPG>
+template <int QT, int M, int R, int D, int WPG, bool LN>
 const void* stream_kernel_ptr() {
-  return reinterpret_cast<const void*>(&gemv_stream_kernel<QT, M, R, D, WPG>);
+  return reinterpret_cast<const void*>(&gemv_stream_kernel<QT, M, R, D, WPG, LN>);
 }
 
-template <int QT, int M, int R, int D, int WPG>
+template <int QT, int M, int R, int D, int WPG, bool LN>
 hipError_t stream_launch(const GemvArgs& a, int groups, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((gemv_stream_kernel<QT, M, R, D, WPG>), dim3(groups),
+  hipLaunchKernelGGL((gemv_stream_kernel<QT, M, R, D, WPG, LN>), dim3(groups),
                      dim3(WPG * 64), lds, stream, a);
   return hipGetLastError();
+}
+
+// One (R, D) variant, with or without the LayerNorm staging.
+template <int QT, int M, int R, int D, int WPG>
+hipError_t stream_variant(const GemvArgs& a, bool ln, int groups, size_t lds,
+                          hipStream_t stream, const void** fn) {
+  if (fn) {
+    *fn = ln ? stream_kernel_ptr<QT, M, R, D, WPG, true>()
+             : stream_kernel_ptr<QT, M, R, D, WPG, false>();
+    return hipSuccess;
+  }
+  return ln ? stream_launch<QT, M, R, D, WPG, true>(a, groups, lds, stream)
+            : stream_launch<QT, M, R, D, WPG, false>(a, groups, lds, stream);
 }
 
 // (R, D) pairs: one row per lane group with an 8-deep ring, or two rows with
 // a 4-deep ring (8 units in flight per lane either way).
 template <int QT, int M, int WPG>
-hipError_t stream_dispatch_r(const GemvArgs& a, int rows, int groups, size_t lds,
+hipError_t stream_dispatch_r(const GemvArgs& a, bool ln, int rows, int groups, size_t lds,
                              hipStream_t stream, const void** fn) {
-  if (rows == 2) {
-    if (fn) { *fn = stream_kernel_ptr<QT, M, 2, 4, WPG>(); return hipSuccess; }
-    return stream_launch<QT, M, 2, 4, WPG>(a, groups, lds, stream);
-  }
-  if (fn) { *fn = stream_kernel_ptr<QT, M, 1, 8, WPG>(); return hipSuccess; }
-  return stream_launch<QT, M, 1, 8, WPG>(a, groups, lds, stream);
+  if (rows == 2) return stream_variant<QT, M, 2, 4, WPG>(a, ln, groups, lds, stream, fn);
+  return stream_variant<QT, M, 1, 8, WPG>(a, ln, groups, lds, stream, fn);
 }
 
 template <int QT, int M>
-hipError_t stream_dispatch_w(const GemvArgs& a, int rows, int wpg, int groups, size_t lds,
-                             hipStream_t stream, const void** fn) {
+hipError_t stream_dispatch_w(const GemvArgs& a, bool ln, int rows, int wpg, int groups,
+                             size_t lds, hipStream_t stream, const void** fn) {
   if (wpg != kStreamWavesPerGroup) return hipErrorInvalidValue;
-  return stream_dispatch_r<QT, M, kStreamWavesPerGroup>(a, rows, groups, lds, stream, fn);
+  return stream_dispatch_r<QT, M, kStreamWavesPerGroup>(a, ln, rows, groups, lds, stream, fn);
 }
 
 template <int QT>
-hipError_t stream_dispatch_m(const GemvArgs& a, int m, int rows, int wpg, int groups,
+hipError_t stream_dispatch_m(const GemvArgs& a, bool ln, int m, int rows, int wpg, int groups,
                              size_t lds, hipStream_t stream, const void** fn) {
   switch (m) {
-    case 1: return stream_dispatch_w<QT, 1>(a, rows, wpg, groups, lds, stream, fn);
-    case 2: return stream_dispatch_w<QT, 2>(a, rows, wpg, groups, lds, stream, fn);
-    case 3: return stream_dispatch_w<QT, 3>(a, rows, wpg, groups, lds, stream, fn);
-    case 4: return stream_dispatch_w<QT, 4>(a, rows, wpg, groups, lds, stream, fn);
-    case 5: return stream_dispatch_w<QT, 5>(a, rows, wpg, groups, lds, stream, fn);
-    case 6: return stream_dispatch_w<QT, 6>(a, rows, wpg, groups, lds, stream, fn);
-    case 7: return stream_dispatch_w<QT, 7>(a, rows, wpg, groups, lds, stream, fn);
-    case 8: return stream_dispatch_w<QT, 8>(a, rows, wpg, groups, lds, stream, fn);
+    case 1: return stream_dispatch_w<QT, 1>(a, ln, rows, wpg, groups, lds, stream, fn);
+    case 2: return stream_dispatch_w<QT, 2>(a, ln, rows, wpg, groups, lds, stream, fn);
+    case 3: return stream_dispatch_w<QT, 3>(a, ln, rows, wpg, groups, lds, stream, fn);
+    case 4: return stream_dispatch_w<QT, 4>(a, ln, rows, wpg, groups, lds, stream, fn);
+    case 5: return stream_dispatch_w<QT, 5>(a, ln, rows, wpg, groups, lds, stream, fn);
+    case 6: return stream_dispatch_w<QT, 6>(a, ln, rows, wpg, groups, lds, stream, fn);
+    case 7: return stream_dispatch_w<QT, 7>(a, ln, rows, wpg, groups, lds, stream, fn);
+    case 8: return stream_dispatch_w<QT, 8>(a, ln, rows, wpg, groups, lds, stream, fn);
   }
   return hipErrorInvalidValue;
 }
 
-hipError_t stream_dispatch(const GemvArgs& a, int qtype, int m, int rows, int wpg, int groups,
-                           size_t lds, hipStream_t stream, const void** fn) {
+hipError_t stream_dispatch(const GemvArgs& a, bool ln, int qtype, int m, int rows, int wpg,
+                           int groups, size_t lds, hipStream_t stream, const void** fn) {
   switch (qtype) {
-    case 4: return stream_dispatch_m<4>(a, m, rows, wpg, groups, lds, stream, fn);
-    case 5: return stream_dispatch_m<5>(a, m, rows, wpg, groups, lds, stream, fn);
-    case 8: return stream_dispatch_m<8>(a, m, rows, wpg, groups, lds, stream, fn);
+    case 4: return stream_dispatch_m<4>(a, ln, m, rows, wpg, groups, lds, stream, fn);
+    case 5: return stream_dispatch_m<5>(a, ln, m, rows, wpg, groups, lds, stream, fn);
+    case 8: return stream_dispatch_m<8>(a, ln, m, rows, wpg, groups, lds, stream, fn);
   }
   return hipErrorInvalidValue;
 }
@@ -273,16 +285,18 @@ size_t stream_lds_bytes(int qtype, int m, int k) {
   return (size_t)m * units * lds_bytes_per_unit(qtype);
 }
 
-const void* stream_kernel(int qtype, int m, int rows, int wpg) {
+const void* stream_kernel(int qtype, int m, int rows, int wpg, bool ln) {
   const void* fn = nullptr;
   GemvArgs unused{};
-  (void)stream_dispatch(unused, qtype, m, rows, wpg, 0, 0, nullptr, &fn);
+  (void)stream_dispatch(unused, ln, qtype, m, rows, wpg, 0, 0, nullptr, &fn);
   return fn;
 }
 
 hipError_t launch_gemv_stream(const GemvArgs& a, int qtype, int m, int rows, int wpg,
                               int groups, hipStream_t stream) {
-  return stream_dispatch(a, qtype, m, rows, wpg, groups, stream_lds_bytes(qtype, m, a.k),
+  return stream_dispatch(a, a.ln_w || a.ln_b, qtype, m, rows, wpg, groups,
+                         stream_lds_bytes(qtype, m, a.k) +
+                             layer_norm_lds_bytes(a.k, a.ln_w || a.ln_b),
                          stream, nullptr);
 }
 

@@ -45,8 +45,12 @@ int units_per_block(int qtype);
 // needs for x and the offset sums, its function pointer (for occupancy
 // queries) and launcher.
 constexpr int kStreamWavesPerGroup = 4;
+// Extra LDS of the streaming kernels for the LayerNorm weight and bias.
+inline size_t layer_norm_lds_bytes(int k, bool ln) {
+  return ln ? (size_t)2 * ((k / 8 + 63) / 64 * 64) * 16 : 0;
+}
 size_t stream_lds_bytes(int qtype, int m, int k);
-const void* stream_kernel(int qtype, int m, int rows, int wpg);
+const void* stream_kernel(int qtype, int m, int rows, int wpg, bool ln = false);
 hipError_t launch_gemv_stream(const GemvArgs& a, int qtype, int m, int rows, int wpg,
                               int groups, hipStream_t stream);
 
@@ -60,7 +64,7 @@ hipError_t launch_gemv_mfma(const GemvArgs& a, int qtype, int m, int rows, int g
 
 // Streaming MFMA kernel (svq_gemv_mfma4.hip), 1 <= M <= 4: function pointer
 // and launcher (LDS layout and size as the vector streaming kernel).
-const void* mfma4_kernel(int qtype, int m, int rows);
+const void* mfma4_kernel(int qtype, int m, int rows, bool ln = false);
 size_t mfma4_lds_bytes(int qtype, int m, int k, int rows, int ksplit);
 hipError_t launch_gemv_mfma4(const GemvArgs& a, int qtype, int m, int rows, int groups,
                              hipStream_t stream);
