@@ -1,7 +1,8 @@
 """Compile libsvq.so (the gfx950 HIP kernels + C ABI) in-tree with hipcc.
 
 Each .hip source under csrc/ becomes an object in _obj/ (compiled in
-parallel), then the objects are linked into libsvq.so next to this file. The
+parallel; the host-only .cpp sources with the host C++ compiler), then the
+objects are linked into libsvq.so next to this file. The
 library is always rebuilt when this runs; callers that only need it loaded use
 `_native.load()`.
 """
@@ -34,9 +35,15 @@ def hipcc() -> str:
     return path
 
 
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-pthread", "-Wall", f"-I{INCLUDE_DIR}"]
+
+
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":  # host-only code (the GGUF reader)
+        cmd = [os.environ.get("CXX") or "g++", *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
@@ -45,7 +52,7 @@ def _compile(src: Path) -> Path:
 
 def build_library(jobs: int | None = None) -> Path:
     """Compile every csrc/*.hip for gfx950 and link libsvq.so; returns its path."""
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     OBJ_DIR.mkdir(exist_ok=True)
@@ -53,7 +60,7 @@ def build_library(jobs: int | None = None) -> Path:
     with ThreadPoolExecutor(max_workers=workers) as pool:
         objects = list(pool.map(_compile, sources))
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", "-o", str(tmp),
            *map(str, objects)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:

@@ -66,6 +66,35 @@ def load() -> ctypes.CDLL:
         lib.svq_decode_attention.argtypes = [vp, i64, vp, vp, vp, vp, i64, vp, vp, i32, vp,
                                              i32, i32, i32, i32, ctypes.c_float, vp, i64, vp]
         lib.svq_decode_attention.restype = i32
+        cp = ctypes.c_char_p
+        lib.svq_gguf_open.argtypes = [cp, i32, ctypes.POINTER(vp)]
+        lib.svq_gguf_open.restype = i32
+        lib.svq_gguf_close.argtypes = [vp]
+        lib.svq_gguf_close.restype = None
+        lib.svq_gguf_version.argtypes = [vp]
+        lib.svq_gguf_version.restype = i32
+        lib.svq_gguf_alignment.argtypes = [vp]
+        lib.svq_gguf_alignment.restype = i64
+        lib.svq_gguf_kv_count.argtypes = [vp]
+        lib.svq_gguf_kv_count.restype = i64
+        lib.svq_gguf_find_kv.argtypes = [vp, cp]
+        lib.svq_gguf_find_kv.restype = i64
+        lib.svq_gguf_kv.argtypes = [vp, i64, ctypes.POINTER(cp), ctypes.POINTER(i32),
+                                    ctypes.POINTER(vp), ctypes.POINTER(i64), ctypes.POINTER(i32),
+                                    ctypes.POINTER(i64)]
+        lib.svq_gguf_kv.restype = i32
+        lib.svq_gguf_tensor_count.argtypes = [vp]
+        lib.svq_gguf_tensor_count.restype = i64
+        lib.svq_gguf_find_tensor.argtypes = [vp, cp]
+        lib.svq_gguf_find_tensor.restype = i64
+        lib.svq_gguf_tensor.argtypes = [vp, i64, ctypes.POINTER(cp), ctypes.POINTER(i32),
+                                        ctypes.POINTER(i32), ctypes.POINTER(i64),
+                                        ctypes.POINTER(i64), ctypes.POINTER(i64)]
+        lib.svq_gguf_tensor.restype = i32
+        lib.svq_gguf_tensor_data.argtypes = [vp, i64]
+        lib.svq_gguf_tensor_data.restype = vp
+        lib.svq_pack_soa.argtypes = [vp, i64, i32, vp, vp, i32]
+        lib.svq_pack_soa.restype = i32
         version = lib.svq_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"libsvq ABI {version}, expected {ABI_VERSION}")
@@ -239,3 +268,74 @@ def decode_attention(qkv: torch.Tensor, cos: torch.Tensor | None, sin: torch.Ten
             out.data_ptr(), rows, heads, kv_heads, head_dim, scale, workspace.data_ptr(),
             workspace.numel(), _stream(qkv.device))
     _check(lib, "svq_decode_attention", rc)
+
+
+def pack_soa(aos_ptr: int, nblocks: int, qtype: str, q: torch.Tensor, s: torch.Tensor,
+             threads: int = 0) -> None:
+    """Host AoS blocks at aos_ptr -> SoA payload q and scale bytes s (uint8 CPU
+    tensors of nblocks * W and nblocks * 2 bytes), on `threads` host threads."""
+    lib = load()
+    _check(lib, "svq_pack_soa", lib.svq_pack_soa(aos_ptr, nblocks, QTYPE_CODE[qtype],
+                                                  q.data_ptr(), s.data_ptr(), threads))
+
+
+class GGUFFile:
+    """A GGUF file opened by the library's reader (svq_gguf_*): metadata and
+    tensor infos, parsed and bounds-checked in C++. Closed on close() or when
+    garbage collected."""
+
+    def __init__(self, path: str, writable_copy: bool = False):
+        self._lib = load()
+        handle = ctypes.c_void_p()
+        rc = self._lib.svq_gguf_open(str(path).encode(), int(writable_copy), ctypes.byref(handle))
+        _check(self._lib, "svq_gguf_open", rc)
+        self._h = handle
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.svq_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def version(self) -> int:
+        return self._lib.svq_gguf_version(self._h)
+
+    @property
+    def alignment(self) -> int:
+        return self._lib.svq_gguf_alignment(self._h)
+
+    def kv_count(self) -> int:
+        return self._lib.svq_gguf_kv_count(self._h)
+
+    def kv(self, i: int):
+        """(key, type, address, nbytes, element type, count) of metadata entry i."""
+        key, typ, val = ctypes.c_char_p(), ctypes.c_int(), ctypes.c_void_p()
+        nbytes, et, count = ctypes.c_int64(), ctypes.c_int(), ctypes.c_int64()
+        _check(self._lib, "svq_gguf_kv", self._lib.svq_gguf_kv(
+            self._h, i, ctypes.byref(key), ctypes.byref(typ), ctypes.byref(val),
+            ctypes.byref(nbytes), ctypes.byref(et), ctypes.byref(count)))
+        return (key.value.decode("utf-8", errors="replace"), typ.value, val.value or 0,
+                nbytes.value, et.value, count.value)
+
+    def find_kv(self, key: str) -> int:
+        return self._lib.svq_gguf_find_kv(self._h, key.encode())
+
+    def tensor_count(self) -> int:
+        return self._lib.svq_gguf_tensor_count(self._h)
+
+    def tensor(self, i: int):
+        """(name, ggml type, dims in file order, file offset, nbytes) of tensor i."""
+        name, typ, nd = ctypes.c_char_p(), ctypes.c_int(), ctypes.c_int()
+        dims = (ctypes.c_int64 * 4)()
+        off, nbytes = ctypes.c_int64(), ctypes.c_int64()
+        _check(self._lib, "svq_gguf_tensor", self._lib.svq_gguf_tensor(
+            self._h, i, ctypes.byref(name), ctypes.byref(typ), ctypes.byref(nd), dims,
+            ctypes.byref(off), ctypes.byref(nbytes)))
+        return (name.value.decode("utf-8", errors="replace"), typ.value,
+                tuple(dims[: nd.value]), off.value, nbytes.value)
+
+    def tensor_address(self, i: int) -> int:
+        return self._lib.svq_gguf_tensor_data(self._h, i) or 0

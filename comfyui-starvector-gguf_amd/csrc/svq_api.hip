@@ -385,6 +385,11 @@ int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t
 
 }  // namespace
 
+namespace svq {
+// Error reporting for the library's host-only sources (svq_gguf.cpp).
+int set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace svq
+
 extern "C" {
 
 int svq_abi_version(void) { return SVQ_ABI_VERSION; }

@@ -113,13 +113,24 @@ def pack_gguf_soa(tensor):
     """Split a GGUF Q4_0/Q5_0/Q8_0 matrix on the CPU into its SoA arrays
     (reference quantization.py:67-90): the block payloads without scales, and
     the fp16 scale bits stored as bytes so that `module.to(dtype)` never
-    converts them."""
+    converts them. Tensors of `gguf_support.GGUFReader` are repacked by the
+    library's multithreaded C++ shuffle; other tensor objects by torch."""
     qtype = type_name(tensor)
     shape = tensor_shape(tensor)
     if qtype not in BLOCK_BYTES or len(shape) != 2 or shape[1] % 32:
         raise ValueError(f"Expected rank-2 GGUF Q4_0/Q5_0/Q8_0 matrix: {tensor.name}")
     block_bytes = BLOCK_BYTES[qtype]
     blocks = shape[0] * (shape[1] // 32)
+    address = getattr(tensor, "native_address", None)
+    if address is not None:
+        # A tensor of this package's GGUF reader: the library repacks straight
+        # from its file mapping on the host threads (svq_pack_soa).
+        if tensor.n_bytes != blocks * block_bytes:
+            raise ValueError(f"Invalid packed GGUF payload: {tensor.name}")
+        q = torch.empty(blocks * (block_bytes - 2), dtype=torch.uint8)
+        scales = torch.empty(blocks * 2, dtype=torch.uint8)
+        _native.pack_soa(address, blocks, qtype, q, scales)
+        return q, scales
     src = torch.from_numpy(np.asarray(tensor.data).view(np.uint8))
     if src.numel() != blocks * block_bytes:
         raise ValueError(f"Invalid packed GGUF payload: {tensor.name}")

@@ -56,6 +56,8 @@ extern "C" {
 #define SVQ_E_ALIGN (-6)   /* x / q / out not aligned for 16-byte accesses
                               (q: 4 bytes for Q5_0; s, bias: 2 bytes) */
 #define SVQ_E_WORKSPACE (-7) /* workspace smaller than the call needs */
+#define SVQ_E_FORMAT (-8)  /* malformed or truncated GGUF file */
+#define SVQ_E_IO (-9)      /* a GGUF file cannot be opened, read or mapped */
 
 /* Activations of svq_gemv_fused. */
 #define SVQ_ACT_NONE 0
@@ -178,6 +180,47 @@ int svq_decode_attention(const uint16_t *qkv, int64_t qkv_stride, const uint16_t
                          int span, uint16_t *out, int rows, int heads, int kv_heads,
                          int head_dim, float scale, void *workspace,
                          int64_t workspace_bytes, void *stream);
+
+/*
+ * GGUF container reader (host memory; no GPU needed). Replaces the PyPI
+ * `gguf` GGUFReader the reference opens its checkpoints with
+ * (gguf_support.py:101-121): GGUF versions 2 and 3, memory-mapped once,
+ * every count, length and offset checked against the file before use.
+ * writable_copy maps the file copy-on-write (the reference's mode "c"):
+ * writes through the mapping stay private to the process.
+ */
+typedef struct svq_gguf svq_gguf;
+int svq_gguf_open(const char *path, int writable_copy, svq_gguf **out);
+void svq_gguf_close(svq_gguf *g);
+int svq_gguf_version(const svq_gguf *g);
+int64_t svq_gguf_alignment(const svq_gguf *g);
+
+/* Metadata entries, in file order. For a string, value points at its bytes
+ * (nbytes long, not NUL-terminated); for an array, at its first element, with
+ * elem_type and count set (string elements keep their u64 length prefixes);
+ * for a scalar, at its little-endian bytes. elem_type is -1 for non-arrays.
+ * Pointers stay valid until svq_gguf_close. */
+int64_t svq_gguf_kv_count(const svq_gguf *g);
+int64_t svq_gguf_find_kv(const svq_gguf *g, const char *key); /* index or -1 */
+int svq_gguf_kv(const svq_gguf *g, int64_t i, const char **key, int *type,
+                const void **value, int64_t *nbytes, int *elem_type, int64_t *count);
+
+/* Tensor infos, in file order: ggml type code, dims (dims[0] varies
+ * fastest, unused dims 1), the byte offset of the data in the file and its
+ * size. svq_gguf_find_tensor returns the first tensor of that name or -1. */
+int64_t svq_gguf_tensor_count(const svq_gguf *g);
+int64_t svq_gguf_find_tensor(const svq_gguf *g, const char *name);
+int svq_gguf_tensor(const svq_gguf *g, int64_t i, const char **name, int *ggml_type,
+                    int *n_dims, int64_t *dims, int64_t *data_offset, int64_t *nbytes);
+const void *svq_gguf_tensor_data(const svq_gguf *g, int64_t i); /* NULL if out of range */
+
+/*
+ * AoS GGUF blocks -> the SoA arrays of `pack_gguf_soa` (quantization.py:67-90):
+ * q[b * W ..] = block b without its 2 scale bytes, s[2b], s[2b + 1] = its fp16
+ * scale bytes. Host memory; `threads` <= 0 uses the hardware threads.
+ */
+int svq_pack_soa(const uint8_t *aos, int64_t nblocks, int qtype, uint8_t *q, uint8_t *s,
+                 int threads);
 
 #ifdef __cplusplus
 }

@@ -16,14 +16,15 @@ HEADER = ROOT / "include" / "svq.h"
 
 def declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int64_t|int|const char \*)\s*(svq_\w+)\s*\(", text,
-                                  re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int64_t|int|void|const char \*|const void \*)\s*(svq_\w+)\s*\(",
+                                  text, re.M)))
 
 
 def test_header_declares_the_entry_points():
     names = declared_functions()
     assert {"svq_abi_version", "svq_last_error", "svq_gemv", "svq_dequant",
-            "svq_dequant_rows", "svq_decode_attention", "svq_gemv_fused",
+            "svq_dequant_rows", "svq_decode_attention", "svq_gemv_fused", "svq_gguf_open",
+            "svq_gguf_close", "svq_gguf_tensor", "svq_gguf_tensor_data", "svq_pack_soa",
             "svq_decode_attention_workspace"} <= set(names)
 
 
