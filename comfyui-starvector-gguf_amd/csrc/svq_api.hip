@@ -199,8 +199,8 @@ constexpr int kMfmaMinRows = 5;  // smallest M sent to the MFMA kernel by defaul
 // per lane) over 16 unit slots. Variant (the `rows` code): 3 = Q5_0 with
 // three consecutive units per lane (needs units % 48 == 0), 2 = two row sets
 // per lane, 1 = one. The 4 waves of a workgroup split K (S = 2 or 4) and add
-// their partial sums through LDS: by default S = 2 when the tiles fill a
-// quarter of the resident waves or fewer, otherwise as SVQ_MFMA_S asks. Workgroups are
+// their partial sums through LDS: by default S = 2 when single-row-set tiles
+// fill a quarter of the resident waves or fewer, otherwise as SVQ_MFMA_S asks. Workgroups are
 // persistent over tile groups, trimmed so that each processes the same number
 // of groups.
 bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_out,
@@ -228,7 +228,9 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
     wmax = cus * waves_per_cu(dev, svq::mfma4_kernel(qtype, m, rows, extra_lds > 0), wpg, lds);
     const int tile_rows = rows == 2 ? 8 : 4;
     tiles = (n + tile_rows - 1) / tile_rows;
-    if (tiles >= wmax || rows != 2 || tu.mfma_r) break;
+    // Two row sets per lane share each x read; measured faster down to an
+    // eighth of the resident waves (Q4_0 / Q8_0 at K = 4608, M = 2..4).
+    if (tiles >= wmax || rows != 2 || tu.mfma_r || 8 * (int64_t)tiles >= wmax) break;
     rows = 1;
   }
   // Long rows with too few tiles to fill the GPU go to the vector kernel,
@@ -238,7 +240,7 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   int ksplit = 1;
   if (tu.mfma_s == 2 || tu.mfma_s == 4) {
     ksplit = tu.mfma_s;
-  } else if (tu.mfma_s == 0 && 4 * (int64_t)tiles <= wmax && steps >= 8) {
+  } else if (tu.mfma_s == 0 && rows == 1 && 4 * (int64_t)tiles <= wmax && steps >= 8) {
     ksplit = 2;  // a quarter of the waves or fewer: halve K per wave
   }
   if (ksplit > steps) ksplit = 1;  // every wave needs at least one step
