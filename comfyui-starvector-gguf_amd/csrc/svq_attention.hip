@@ -18,11 +18,11 @@
 // fp16(rotate_half(x) * sin)), each product and the sum formed in fp32.
 //
 // Work split (flash decoding), two kernels:
-// 1. Workgroup (c, r) takes cache chunk c (64 slots) of (row, kv head) r. Its
-//    4 waves take 16 slots each; a 16-lane row of a wave holds one slot, lane
-//    p of the row dims 8p..8p+7 of q, k and v. It writes the chunk's max
-//    score, sum of exponentials and weighted sum of V per query head to the
-//    workspace.
+// 1. Workgroup (c, r) takes cache chunk c (128 slots) of (row, kv head) r;
+//    each of its 4 waves computes the scores and the weighted V sums of 32
+//    slots on the matrix cores (see decode_attention_kernel). It writes the
+//    chunk's max score, sum of exponentials and weighted sum of V per query
+//    head to the workspace.
 // 2. One workgroup per (row, query head) merges the chunks and writes the
 //    output. The kernel boundary orders the two: no atomics, no fences.
 #include <math.h>
@@ -36,8 +36,7 @@ namespace {
 
 constexpr int kD = 128;                        // head dimension
 constexpr int kWaves = 4;
-constexpr int kIters = 4;                      // slots per 16-lane row
-constexpr int kChunk = kWaves * 4 * kIters;    // slots per workgroup
+constexpr int kChunk = kWaves * 32;            // slots per workgroup (32 per wave)
 constexpr uint32_t kOutOfRange = 0x80000000u;  // past every buffer range
 
 __device__ __forceinline__ u32x4 load16(const uint16_t* p) {
@@ -56,15 +55,20 @@ __device__ __forceinline__ uint32_t pack_halves(_Float16 lo, _Float16 hi) {
 }
 
 // One rotated element: fp16(fp16(x * c) + fp16(r * s)), r = -partner for the
-// lower half of the head dims and +partner for the upper half. Contraction is
-// off: a fused multiply-add would skip the rounding of the products.
+// lower half of the head dims and +partner for the upper half. In fp16
+// arithmetic: an fp16 product or sum is the correctly rounded exact result,
+// which is what the reference's ops give (each formed exactly in fp32 -- the
+// product always, the sum whenever rounding can matter -- then rounded).
+// Contraction is off: a fused multiply-add would skip the product rounding.
 __device__ __forceinline__ _Float16 rope1(_Float16 x, _Float16 partner, _Float16 c,
                                           _Float16 s, bool lower) {
 #pragma clang fp contract(off)
-  const float r = lower ? -(float)partner : (float)partner;
-  const _Float16 a = (_Float16)((float)x * (float)c);
-  const _Float16 b = (_Float16)(r * (float)s);
-  return (_Float16)((float)a + (float)b);
+  // Sign flip on the bits: exactly torch's negation, -0 for +0 included.
+  const _Float16 r = __builtin_bit_cast(
+      _Float16, (uint16_t)(__builtin_bit_cast(uint16_t, partner) ^ (lower ? 0x8000u : 0u)));
+  const _Float16 a = x * c;
+  const _Float16 b = r * s;
+  return a + b;
 }
 
 __device__ __forceinline__ uint32_t rope2(uint32_t x, uint32_t partner, uint32_t c,
@@ -82,10 +86,6 @@ __device__ __forceinline__ u32x4 rope8(u32x4 x, u32x4 partner, u32x4 c, u32x4 s,
   return r;
 }
 
-__device__ __forceinline__ float dot8(u32x4 a, u32x4 b) {
-  return dot2(a.w, b.w, dot2(a.z, b.z, dot2(a.y, b.y, dot2(a.x, b.x, 0.0f))));
-}
-
 // Combine v over the four 16-lane rows of a wave (same lane position in each
 // row) with the gfx950 lane swaps; every lane receives the result.
 template <bool kMax>
@@ -101,162 +101,202 @@ __device__ __forceinline__ float rows_reduce(float v) {
   return kMax ? fmaxf(a, b) : a + b;
 }
 
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4_t mfma16x16x32(u32x4 a, u32x4 b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a),
+                                                __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
+}
+
+// Chunk kernel. Wave w takes the 32 slots s0 = c0 + 32w .. s0 + 31 as two
+// 16-slot tiles. Lane (n = lane % 16, g = lane / 16):
+// * S = K Q^T on v_mfma_f32_16x16x32_f16, four k-steps of 32 dims: A = K
+//   (row n = slot, k-slots = dims 32 ks + 8g .. + 7), B = Q^T (column n =
+//   query head n of the group, same dims). D gives the lane head n and
+//   slots 4g + i, i < 4, of each tile.
+// * O = P V on the same instruction, eight 16-dim tiles: A = P (row n = head,
+//   k-slot (g, e) = slot 4g + e of tile 0 for e < 4, of tile 1 for e >= 4:
+//   exactly the scores the lane holds), B = V read back from LDS at the same
+//   slots (column n = dim). D gives the lane dim 16dt + n of heads 4g + i.
+// Heads n >= G compute on zero queries and are never stored.
 template <int G>
 __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs a) {
-  __shared__ float red[kWaves][G];
-  __shared__ float accs[kWaves][G][kD + 4];
+  constexpr int kVRow = kD / 8 + 1;  // u32x4 per staged V row (one of padding)
+  constexpr int kVBytes = kWaves * 32 * kVRow * 16;
+  constexpr int kOBytes = kWaves * 16 * (kD + 4) * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kVBytes > kOBytes ? kVBytes : kOBytes];
+  __shared__ float red[kWaves][16], lsum[kWaves][16];
+  u32x4* vst = reinterpret_cast<u32x4*>(smem);  // [wave][32 slots][kVRow]
+  float* ost = reinterpret_cast<float*>(smem);  // [wave][16 heads][kD + 4]
 
   const int c = blockIdx.x;
   const int rk = blockIdx.y;
   const int row = rk / a.kv_heads, kv = rk - row * a.kv_heads;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int p = lane & 15, sl = lane >> 4;
+  const int n = lane & 15, g = lane >> 4;
   const int64_t pos = *a.position;
   const int heads = a.kv_heads * G;
-
-  // q of the G query heads of this kv head, and the new k and v, rotated.
-  const uint16_t* qrow = a.qkv + (int64_t)row * a.qkv_stride;
   const bool rope = a.cos != nullptr;
-  const bool lower = p < 8;
-  const int partner = (8 * p + kD / 2) & (kD - 1);
-  u32x4 cs = {0, 0, 0, 0}, sn = {0, 0, 0, 0};
-  if (rope) {
-    cs = load16(a.cos + 8 * p);
-    sn = load16(a.sin + 8 * p);
-  }
-  u32x4 qv[G];
+
+  // Rotation of a lane's 4 pieces (dims 32 ks + 8g): the partner of piece ks
+  // is piece ks ^ 2 (dims + 64 mod 128); the lower half of the dims is ks < 2.
+  auto rotate4 = [&](u32x4 (&v)[4]) {
+    if (!rope) return;
+    u32x4 r[4];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const uint16_t* qh = qrow + (kv * G + g) * kD;
-    qv[g] = load16(qh + 8 * p);
-    if (rope) qv[g] = rope8(qv[g], load16(qh + partner), cs, sn, lower);
+    for (int ks = 0; ks < 4; ++ks) {
+      const int d = 32 * ks + 8 * g;
+      r[ks] = rope8(v[ks], v[ks ^ 2], load16(a.cos + d), load16(a.sin + d), ks < 2);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) v[ks] = r[ks];
+  };
+
+  // Q^T (B of the score MFMAs): query head kv * G + n, zero for n >= G.
+  const uint16_t* qrow = a.qkv + (int64_t)row * a.qkv_stride;
+  u32x4 qb[4];
+  const uint16_t* qh = qrow + (kv * G + (n < G ? n : 0)) * kD;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qb[ks] = load16(qh + 32 * ks + 8 * g);
+  rotate4(qb);
+  if (n >= G) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qb[ks] = u32x4{0, 0, 0, 0};
   }
+  // The new key (rotated) and value at this lane's dims.
+  u32x4 kn[4], vn[4];
   const uint16_t* krow = qrow + (heads + kv) * kD;
   const uint16_t* vrow = qrow + (heads + a.kv_heads + kv) * kD;
-  u32x4 knew = load16(krow + 8 * p);
-  if (rope) knew = rope8(knew, load16(krow + partner), cs, sn, lower);
-  const u32x4 vnew = load16(vrow + 8 * p);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    kn[ks] = load16(krow + 32 * ks + 8 * g);
+    vn[ks] = load16(vrow + 32 * ks + 8 * g);
+  }
+  rotate4(kn);
 
   const int64_t slab = (int64_t)rk * a.capacity * kD;
   uint16_t* kslab = a.keys + slab;
   uint16_t* vslab = a.values + slab;
-  const int c0 = c * kChunk;
-  if (w == 0 && sl == 0 && pos >= c0 && pos < c0 + kChunk && pos < a.span) {
-    *reinterpret_cast<u32x4*>(kslab + pos * kD + 8 * p) = knew;
-    *reinterpret_cast<u32x4*>(vslab + pos * kD + 8 * p) = vnew;
-  }
-
-  // This lane's slots: c0 + w * 16 + it * 4 + sl. Masked slots (past the span
-  // or with a -inf bias) and the new slot load nothing.
+  const int c0 = c * kChunk, s0 = c0 + 32 * w;
   const __amdgpu_buffer_rsrc_t kr = make_rsrc(kslab, (uint32_t)a.span * kD * 2);
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(vslab, (uint32_t)a.span * kD * 2);
-  u32x4 kk[kIters], vv[kIters];
-  float bias[kIters];
+
+  // K (A of the score MFMAs) and V (staged to LDS) of slot s0 + 16t + n.
+  // Masked slots (past the span or with a -inf bias) and the new slot load
+  // nothing; the new slot takes kn / vn and is written to the cache.
+  u32x4 ka[2][4], va[2][4];
 #pragma unroll
-  for (int it = 0; it < kIters; ++it) {
-    const int j = c0 + w * 16 + it * 4 + sl;
-    float b = -INFINITY;
-    if (j < a.span) b = a.bias ? half_bits_to_float(a.bias[j]) : 0.0f;
-    bias[it] = b;
-    const bool load = b != -INFINITY && j != pos;
-    const uint32_t off = load ? (uint32_t)j * kD * 2 + 16u * p : kOutOfRange;
-    kk[it] = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
-    vv[it] = __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0);
-  }
+  for (int t = 0; t < 2; ++t) {
+    const int j = s0 + 16 * t + n;
+    bool load = j < a.span && j != pos;
+    if (load && a.bias) load = half_bits_to_float(a.bias[j]) != -INFINITY;
 #pragma unroll
-  for (int it = 0; it < kIters; ++it) {
-    if (c0 + w * 16 + it * 4 + sl == pos) {
-      kk[it] = knew;
-      vv[it] = vnew;
+    for (int ks = 0; ks < 4; ++ks) {
+      const uint32_t off = load ? (uint32_t)j * kD * 2 + (32u * ks + 8u * g) * 2 : kOutOfRange;
+      ka[t][ks] = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
+      va[t][ks] = __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0);
     }
   }
-
-  // Scores, rounded to fp16 as the reference's fp16 baddbmm output.
-  float sc[kIters][G];
 #pragma unroll
-  for (int it = 0; it < kIters; ++it) {
+  for (int t = 0; t < 2; ++t) {
+    const int j = s0 + 16 * t + n;
+    if (j == pos && pos < a.span) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float d = group_sum(dot8(qv[g], kk[it]), 4);
-      sc[it][g] = bias[it] == -INFINITY ? -INFINITY
-                                        : (float)(_Float16)(fmaf(a.scale, d, bias[it]));
+      for (int ks = 0; ks < 4; ++ks) {
+        ka[t][ks] = kn[ks];
+        va[t][ks] = vn[ks];
+        *reinterpret_cast<u32x4*>(kslab + pos * kD + 32 * ks + 8 * g) = kn[ks];
+        *reinterpret_cast<u32x4*>(vslab + pos * kD + 32 * ks + 8 * g) = vn[ks];
+      }
     }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) vst[(w * 32 + 16 * t + n) * kVRow + 4 * ks + g] = va[t][ks];
   }
 
-  // Chunk max per head.
-  float m[G];
+  // Scores of head n at slots 4g + i of each tile, rounded to fp16 as the
+  // reference's fp16 baddbmm output.
+  float sc[2][4];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float v = sc[0][g];
+  for (int t = 0; t < 2; ++t) {
+    f4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int it = 1; it < kIters; ++it) v = fmaxf(v, sc[it][g]);
-    m[g] = rows_reduce<true>(v);
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) red[w][g] = m[g];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-    m[g] = fmaxf(fmaxf(red[0][g], red[1][g]), fmaxf(red[2][g], red[3][g]));
-
-  // Exponentials and the weighted sum of V over the chunk.
-  float l[G], acc[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
-  }
-#pragma unroll
-  for (int it = 0; it < kIters; ++it) {
-    float vf[8];
-    const uint32_t vw[4] = {vv[it].x, vv[it].y, vv[it].z, vv[it].w};
+    for (int ks = 0; ks < 4; ++ks) d = mfma16x16x32(ka[t][ks], qb[ks], d);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      vf[2 * i] = (float)lo_half(vw[i]);
-      vf[2 * i + 1] = (float)hi_half(vw[i]);
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float e = sc[it][g] == -INFINITY ? 0.0f : __expf(sc[it][g] - m[g]);
-      l[g] += e;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(e, vf[i], acc[g][i]);
+      const int j = s0 + 16 * t + 4 * g + i;
+      float b = -INFINITY;
+      if (j < a.span) b = a.bias ? half_bits_to_float(a.bias[j]) : 0.0f;
+      sc[t][i] = b == -INFINITY ? -INFINITY : (float)(_Float16)(fmaf(a.scale, d[i], b));
     }
   }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] = rows_reduce<false>(l[g]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[g][i] = rows_reduce<false>(acc[g][i]);
-  }
-  if (sl == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) accs[w][g][8 * p + i] = acc[g][i];
-      if (p == 0) accs[w][g][kD] = l[g];
-    }
-  }
-  __syncthreads();
 
-  // This chunk's partial per head: (max, sum of exponentials) and the
-  // weighted sum of V.
+  // Chunk max per head: the lane's 8 slots, the 4 lane groups, the 4 waves.
+  float m = sc[0][0];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m = fmaxf(m, sc[t][i]);
+  m = rows_reduce<true>(m);
+  if (g == 0) red[w][n] = m;
+  __syncthreads();  // also orders the V staging before the reads below
+  m = fmaxf(fmaxf(red[0][n], red[1][n]), fmaxf(red[2][n], red[3][n]));
+
+  // P in fp16 (A of the PV MFMAs) and its fp32 sum.
+  float l = 0.f;
+  uint32_t pa[4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    float e[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      e[i] = sc[t][i] == -INFINITY ? 0.0f : __expf(sc[t][i] - m);
+      l += e[i];
+    }
+    pa[2 * t] = pack_halves((_Float16)e[0], (_Float16)e[1]);
+    pa[2 * t + 1] = pack_halves((_Float16)e[2], (_Float16)e[3]);
+  }
+  l = rows_reduce<false>(l);
+  if (g == 0) lsum[w][n] = l;
+  const u32x4 pav = u32x4{pa[0], pa[1], pa[2], pa[3]};
+
+  // O = P V per 16-dim tile; B gathers V[slot 4g + e (tile 0) / 16 + 4g + e - 4
+  // (tile 1)][16 dt + n] from the wave's staged rows.
+  const uint16_t* vw = reinterpret_cast<const uint16_t*>(vst + w * 32 * kVRow);
+  f4_t o[kD / 16];
+#pragma unroll
+  for (int dt = 0; dt < kD / 16; ++dt) {
+    const int dim = 16 * dt + n;
+    uint32_t bv[4];
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      const int sa = (e2 < 2 ? 4 * g + 2 * e2 : 16 + 4 * g + 2 * (e2 - 2));
+      const uint16_t lo = vw[sa * kVRow * 8 + dim], hi = vw[(sa + 1) * kVRow * 8 + dim];
+      bv[e2] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    o[dt] = mfma16x16x32(pav, u32x4{bv[0], bv[1], bv[2], bv[3]}, f4_t{0.f, 0.f, 0.f, 0.f});
+  }
+  __syncthreads();  // the V staging area becomes the O staging area
+
+  // Sum of the 4 waves' O, then this chunk's partial per head < G:
+  // (max, sum of exponentials) and the weighted sum of V.
+#pragma unroll
+  for (int dt = 0; dt < kD / 16; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ost[(w * 16 + 4 * g + i) * (kD + 4) + 16 * dt + n] = o[dt][i];
+  __syncthreads();
   const int64_t head0 = (int64_t)rk * G;
   for (int e = tid; e < G * kD; e += kWaves * 64) {
-    const int g = e / kD, i = e - g * kD;
-    a.acc[((head0 + g) * a.nchunks + c) * kD + i] =
-        accs[0][g][i] + accs[1][g][i] + accs[2][g][i] + accs[3][g][i];
-  }
+    const int h = e / kD, d = e - h * kD;
+    float v = 0.f;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (tid == g) {
-      const float l_sum = accs[0][g][kD] + accs[1][g][kD] + accs[2][g][kD] + accs[3][g][kD];
-      a.ml[(head0 + g) * a.nchunks + c] = make_float2(m[g], l_sum);
-    }
+    for (int ww = 0; ww < kWaves; ++ww) v += ost[(ww * 16 + h) * (kD + 4) + d];
+    a.acc[((head0 + h) * a.nchunks + c) * kD + d] = v;
   }
+  // Thread tid < G holds head n = tid's chunk max in m.
+  if (tid < G)
+    a.ml[(head0 + tid) * a.nchunks + c] =
+        make_float2(m, lsum[0][tid] + lsum[1][tid] + lsum[2][tid] + lsum[3][tid]);
 }
 
 // Merge of the chunk partials of one query head (workgroup (row, h)): lane
