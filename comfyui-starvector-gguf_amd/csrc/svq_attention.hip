@@ -315,6 +315,19 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnMerge a) {
   const float2* ml = a.ml + (int64_t)head * n;
   const float* acc = a.acc + (int64_t)head * n * kD;
 
+  // The first batch of partial loads goes out before the chunk weights are
+  // known: both then take one round trip.
+  float4 v[4];
+  auto load_batch = [&](int ch0) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int ch = ch0 + b * kMergeSlices;
+      v[b] = ch < n ? *reinterpret_cast<const float4*>(acc + (int64_t)ch * kD + d4)
+                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  };
+  load_batch(slice);
+
   if (tid < 64) {
     float mx = -INFINITY;
     for (int ch = tid; ch < n; ch += 64) mx = fmaxf(mx, ml[ch].x);
@@ -322,10 +335,10 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnMerge a) {
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     float sum = 0.0f;
     for (int ch = tid; ch < n; ch += 64) {
-      const float2 v = ml[ch];
-      const float w = v.x == -INFINITY ? 0.0f : __expf(v.x - mx);
+      const float2 c = ml[ch];
+      const float w = c.x == -INFINITY ? 0.0f : __expf(c.x - mx);
       wts[ch] = w;
-      sum = fmaf(v.y, w, sum);
+      sum = fmaf(c.y, w, sum);
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
@@ -334,14 +347,7 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnMerge a) {
   __syncthreads();
 
   float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
-  for (int ch0 = slice; ch0 < n; ch0 += 4 * kMergeSlices) {
-    float4 v[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int ch = ch0 + b * kMergeSlices;
-      v[b] = ch < n ? *reinterpret_cast<const float4*>(acc + (int64_t)ch * kD + d4)
-                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
+  for (int ch0 = slice;;) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int ch = ch0 + b * kMergeSlices;
@@ -351,6 +357,9 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnMerge a) {
       o2 = fmaf(v[b].z, w, o2);
       o3 = fmaf(v[b].w, w, o3);
     }
+    ch0 += 4 * kMergeSlices;
+    if (ch0 >= n) break;
+    load_batch(ch0);
   }
   red[slice][d4] = o0;
   red[slice][d4 + 1] = o1;

@@ -304,12 +304,24 @@ class CachedDecoding:
         return logits
 
     def reorder(self, parents):
-        """Copy each row's parent beam cache into rows that changed parent."""
-        rows = [row for row, parent in enumerate(parents) if parent != row]
-        if rows:
-            sources = [parents[row] for row in rows]
-            self.keys[:, rows, ..., :self.length, :] = self.keys[:, sources, ..., :self.length, :]
-            self.values[:, rows, ..., :self.length, :] = self.values[:, sources, ..., :self.length, :]
+        """Give every row the cache of its parent beam (runtime_shared.py:388-394).
+        A row whose parent is not itself being overwritten is copied slice to
+        slice (one read and one write of its cache); rows that exchange caches
+        gather their sources first, as indexing with the parent list does."""
+        moves = [(row, parent) for row, parent in enumerate(parents) if parent != row]
+        if not moves:
+            return
+        n = self.length
+        targets = {row for row, _ in moves}
+        if any(parent in targets for _, parent in moves):
+            rows = [row for row, _ in moves]
+            sources = [parent for _, parent in moves]
+            for cache in (self.keys, self.values):
+                cache[:, rows, :, :n] = cache[:, sources, :, :n]
+            return
+        for row, parent in moves:
+            for cache in (self.keys, self.values):
+                cache[:, row, :, :n].copy_(cache[:, parent, :, :n])
 
 
 def penalize(scores, seen):

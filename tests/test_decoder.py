@@ -115,3 +115,20 @@ def test_graph_replays_match_eager_decode(cuda_device):
             assert len(decoding.graphs) == 1
             err = ((got - want).abs().max() / want.abs().max()).item()
             assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("parents", ([0, 0, 2], [1, 1, 1], [1, 0, 2], [2, 0, 1], [0, 1, 2]))
+def test_reorder_matches_indexing(parents):
+    """Slice copies and the gather path give each row its parent's cache, as
+    indexing the cache with the parent list does (runtime_shared.py:388-394)."""
+    from starvector_amd.decoder import CachedDecoding
+    g = torch.Generator().manual_seed(4)
+    keys = torch.randn((2, 3, 2, 10, 4), generator=g)
+    values = torch.randn((2, 3, 2, 10, 4), generator=g)
+    decoding = CachedDecoding.__new__(CachedDecoding)
+    decoding.keys, decoding.values, decoding.length = keys.clone(), values.clone(), 7
+    decoding.reorder(parents)
+    for cache, original in ((decoding.keys, keys), (decoding.values, values)):
+        want = original.clone()
+        want[:, :, :, :7] = original[:, parents, :, :7]
+        assert torch.equal(cache, want)
