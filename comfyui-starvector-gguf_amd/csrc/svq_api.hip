@@ -196,9 +196,9 @@ bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out
 constexpr int kMfmaMinRows = 5;  // smallest M sent to the MFMA kernel by default
 
 // Streaming MFMA launch (M <= 4): row tiles of 4 rows (8 with two row sets
-// per lane) over 16 unit slots. Variant (the `rows` code): 3 = Q5_0 with
-// three consecutive units per lane (needs units % 48 == 0), 2 = two row sets
-// per lane, 1 = one. The 4 waves of a workgroup split K (S = 2 or 4) and add
+// per lane) over 16 unit slots. Variant (the `rows` code): 3 = consecutive
+// units per lane (three Q4_0 / Q5_0 blocks, needs units % 48 == 0; one Q8_0
+// block), 2 = two row sets per lane, 1 = one. The 4 waves of a workgroup split K (S = 2 or 4) and add
 // their partial sums through LDS: by default S = 2 when single-row-set tiles
 // fill a quarter of the resident waves or fewer, otherwise as SVQ_MFMA_S asks. Workgroups are
 // persistent over tile groups, trimmed so that each processes the same number
@@ -208,18 +208,26 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   if ((tu.path != 4 && tu.path != 0) || m > 4) return false;
   // Automatic choice (measured at the StarCoder2-8B and GPTBigCode-1B shapes):
   // the matrix-core path wins for Q5_0 at every M and for Q4_0 / Q8_0 from
-  // M = 2; at M = 1 the vector path's dot products are cheap enough.
-  if (tu.path == 0 && qtype != SVQ_Q5_0 && m < 2) return false;
+  // M = 2; at M = 1 the vector path's dot products are cheap enough, except
+  // on matrices of 32 MiB or less, where the shorter prologue of this kernel
+  // wins (4608 x 4608 and 5632 x 4608).
   const uint64_t q_bytes = (uint64_t)n * (k / 32) * payload_bytes(qtype);
+  if (tu.path == 0 && qtype != SVQ_Q5_0 && m < 2 && (q_bytes > (32u << 20) || k > 8192))
+    return false;
   if (q_bytes >= (1ull << 31) || (uint64_t)n * (k / 16) >= (1ull << 31)) return false;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   const int cus = device_cus(dev);
   const int wpg = svq::kStreamWavesPerGroup;
   const int units = (k / 32) * svq::units_per_block(qtype);
-  const bool triple = qtype == SVQ_Q5_0 && units % 48 == 0;
-  int rows = tu.mfma_r ? tu.mfma_r : (triple ? 3 : 2);
-  if (rows == 3 && !triple) rows = 2;
+  // Variant 3 reads consecutive units per lane: three blocks (Q4_0 / Q5_0,
+  // whole steps only: units % 48 == 0) or one Q8_0 block (two units).
+  const bool multi = qtype == SVQ_Q8_0 || units % 48 == 0;
+  const int unit_run = qtype == SVQ_Q8_0 ? 2 : 3;
+  // Defaults: variant 3 for Q5_0 and Q8_0 (measured 2-9% faster than two row
+  // sets at K = 4608 and 18432); Q4_0 keeps two row sets, which share each x read.
+  int rows = tu.mfma_r ? tu.mfma_r : (qtype != SVQ_Q4_0 && multi ? 3 : 2);
+  if (rows == 3 && !multi) rows = 2;
   int wmax = 0, tiles = 0;
   size_t lds = 0;
   for (;;) {
@@ -234,14 +242,20 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
     rows = 1;
   }
   // Long rows with too few tiles to fill the GPU go to the vector kernel,
-  // which spreads a row over 64 lanes: measured faster than splitting K here.
-  if (tu.path == 0 && k > 8192 && tiles < wmax) return false;
-  const int steps = (units + 16 * (rows == 3 ? 3 : 1) - 1) / (16 * (rows == 3 ? 3 : 1));
+  // which spreads a row over 64 lanes: measured faster than splitting K here,
+  // except for Q8_0 whole-block lanes split in two (4608 x 18432, M = 2:
+  // 24.8 us against 27.8 us).
+  const bool long_q8 = qtype == SVQ_Q8_0 && rows == 3 && k > 8192;
+  if (tu.path == 0 && k > 8192 && tiles < wmax && !long_q8) return false;
+  const int per_step = 16 * (rows == 3 ? unit_run : 1);
+  const int steps = (units + per_step - 1) / per_step;
   int ksplit = 1;
   if (tu.mfma_s == 2 || tu.mfma_s == 4) {
     ksplit = tu.mfma_s;
   } else if (tu.mfma_s == 0 && rows == 1 && 4 * (int64_t)tiles <= wmax && steps >= 8) {
     ksplit = 2;  // a quarter of the waves or fewer: halve K per wave
+  } else if (tu.mfma_s == 0 && long_q8) {
+    ksplit = 2;
   }
   if (ksplit > steps) ksplit = 1;  // every wave needs at least one step
   const int slots = wpg / ksplit;

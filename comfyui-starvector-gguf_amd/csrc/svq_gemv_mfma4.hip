@@ -84,9 +84,10 @@ __device__ __forceinline__ float slot_sum(float v) {
 template <int QT, int M, int R, int D, int WPG, int U, bool LN>
 __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   static_assert(M >= 1 && M <= 4, "A has 4 rows");
-  static_assert(U == 1 || (U == 3 && QT == 5), "three units per lane: Q5_0 only");
+  static_assert(U == 1 || (U == 3 && QT != 8) || (U == 2 && QT == 8),
+                "consecutive units per lane: three Q4_0 / Q5_0 blocks or one Q8_0 block");
   using T = QTraits<QT>;
-  constexpr int kWordsU = U == 3 ? 15 : T::kWords;  // payload dwords per lane per step
+  constexpr int kWordsU = U * T::kWords;  // payload dwords per lane per step
   constexpr int J = T::kUnitWeights / 4;  // MFMAs per unit
   extern __shared__ u32x4 lds[];
   __shared__ u32x2 q5_table[QT == 5 ? 256 : 1];
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   };
 
   uint32_t w[D][R][kWordsU];
-  uint32_t sc[D][R][U == 3 ? 2 : 1];
+  uint32_t sc[D][R][U == 3 ? 2 : 1];  // U = 3: block u's scale, then u + 1 and u + 2
   int pj = 0, pit = st0;
   uint32_t pqo[R], pso[R];
   row_offsets(tile_of(0), pqo, pso);
@@ -154,7 +155,8 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
     const uint32_t oob = (uint32_t)(!valid) * kOutOfRange;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if constexpr (U == 3) {
+      if constexpr (U == 3 && QT == 5) {
+        // Three 20-byte blocks: 60 contiguous bytes as 3 x 16 + 12.
         typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
         const uint32_t off = pqo[r] + (uint32_t)u * 20u + oob;
 #pragma unroll
@@ -167,9 +169,26 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
         const u32x3 t = __builtin_bit_cast(
             u32x3, __builtin_amdgcn_raw_buffer_load_b96(qr, off + 48u, 0, 0));
         w[d][r][12] = t.x; w[d][r][13] = t.y; w[d][r][14] = t.z;
+      } else if constexpr (U > 1) {
+        // U consecutive 16-byte units: U x 16 contiguous bytes.
+        const uint32_t off = pqo[r] + (uint32_t)u * 16u + oob;
+#pragma unroll
+        for (int c = 0; c < U; ++c) {
+          const u32x4 v = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off + 16u * c, 0, 0));
+          w[d][r][4 * c] = v.x; w[d][r][4 * c + 1] = v.y;
+          w[d][r][4 * c + 2] = v.z; w[d][r][4 * c + 3] = v.w;
+        }
+      }
+      if constexpr (U == 3) {
+        // Three consecutive blocks (one unit each): their three scales.
         const uint32_t soff = pso[r] + (uint32_t)u * 2u + oob;
         sc[d][r][0] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff, 0, 0);
         sc[d][r][1] = __builtin_amdgcn_raw_buffer_load_b32(sr, soff + 2u, 0, 0);
+      } else if constexpr (U == 2) {
+        // The two halves of one Q8_0 block (u even): one scale.
+        sc[d][r][0] = __builtin_amdgcn_raw_buffer_load_b16(
+            sr, pso[r] + (uint32_t)(u / 2) * 2u + oob, 0, 0);
       } else {
         load_unit_buf<QT>(qr, pqo[r] + (uint32_t)u * T::kUnitBytes + oob, w[d][r]);
         sc[d][r][0] = __builtin_amdgcn_raw_buffer_load_b16(
@@ -249,7 +268,8 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
                                                        __builtin_bit_cast(h4_t, bv), dv, 0, 0, 0);
             }
             // Scale of unit q: the 2-byte load, then the two halves of the 4-byte one.
-            const uint32_t sbits = q == 0 ? sc[d][r][0] : sc[d][r][U == 3 ? 1 : 0] >> (16 * (q - 1));
+            const uint32_t sbits =
+                U != 3 || q == 0 ? sc[d][r][0] : sc[d][r][1] >> (16 * (q - 1));
             const float scale = half_bits_to_float((uint16_t)sbits);
 #pragma unroll
             for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fmaf(dv[m], scale, acc[r][m]);
@@ -338,13 +358,15 @@ hipError_t mfma4_variant(const GemvArgs& a, bool ln, int groups, size_t lds, hip
 }
 
 // rows 1: one row set per lane with an 8-deep ring; rows 2: two row sets
-// (sharing each x read) with a 4-deep ring; rows 3 (Q5_0): one row set, three
-// consecutive units per lane, a 3-deep ring (9 units in flight).
+// (sharing each x read) with a 4-deep ring; rows 3: one row set, consecutive
+// units per lane: three Q4_0 / Q5_0 blocks with a 3-deep ring (9 units in
+// flight) or one Q8_0 block (two units) with a 4-deep ring.
 template <int QT, int M>
 hipError_t mfma4_dispatch_r(const GemvArgs& a, bool ln, int rows, int groups, size_t lds,
                             hipStream_t stream, const void** fn) {
-  if constexpr (QT == 5) {
-    if (rows == 3) return mfma4_variant<QT, M, 1, 3, 3>(a, ln, groups, lds, stream, fn);
+  if (rows == 3) {
+    if constexpr (QT == 8) return mfma4_variant<QT, M, 1, 4, 2>(a, ln, groups, lds, stream, fn);
+    else return mfma4_variant<QT, M, 1, 3, 3>(a, ln, groups, lds, stream, fn);
   }
   if (rows == 2) return mfma4_variant<QT, M, 2, 4, 1>(a, ln, groups, lds, stream, fn);
   return mfma4_variant<QT, M, 1, 8, 1>(a, ln, groups, lds, stream, fn);

@@ -355,8 +355,9 @@ def test_gemv_every_mfma_launch_shape(cuda_device, monkeypatch, rows, ksplit):
 
 @pytest.mark.parametrize("rows", (1, 2, 3))
 def test_gemv_mfma4_row_sets(cuda_device, monkeypatch, rows):
-    """Every variant of the streaming MFMA kernel on ragged shapes (3: three
-    consecutive Q5_0 units per lane, for K a multiple of 1536)."""
+    """Every variant of the streaming MFMA kernel on ragged shapes (3:
+    consecutive units per lane: three Q4_0 / Q5_0 blocks, for K a multiple of
+    1536, or one Q8_0 block)."""
     monkeypatch.setenv("SVQ_PATH", "mfma4")
     monkeypatch.setenv("SVQ_MFMA_R", str(rows))
     rng = np.random.default_rng(rows)
@@ -366,8 +367,7 @@ def test_gemv_mfma4_row_sets(cuda_device, monkeypatch, rows):
             shapes = ((1, 77, 1536), (2, 130, 4608), (3, 3, 3072), (4, 261, 1536))
         for m, n, k in shapes:
             say(f"gemv mfma4 rows={rows} {qtype} m={m} n={n} k={k}")
-            want = rows if rows != 3 or qtype == "Q5_0" else 2
-            assert native.gemv_plan(m, n, k, qtype)["rows"] == want
+            assert native.gemv_plan(m, n, k, qtype)["rows"] == rows
             q, s = orc.synthetic_soa(qtype, n, k, seed=m * n + k)
             x = rng.standard_normal((m, k)).astype(np.float16)
             bias = rng.standard_normal(n).astype(np.float16)
