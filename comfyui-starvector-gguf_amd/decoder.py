@@ -344,11 +344,55 @@ def warp(scores, temperature, top_p, keep):
     return scores
 
 
+# Candidates kept per row by `warp_candidates`: the top-k plus room for values
+# tied with the k-th largest.
+TIE_ROOM = 14
+
+
+def warp_candidates(scores, temperature, top_p, keep):
+    """`warp` computed on each row's top-k candidates instead of the whole
+    vocabulary: the same temperature, top-k threshold and top-p removal
+    (runtime_shared.py:176-187), where the reference's full-vocabulary sort,
+    softmax and cumulative sum become ones over about 64 values per row.
+    Every entry below the k-th largest value is -inf in both, and softmax and
+    cumulative sum over the ascending order only add exact zeros for them, so
+    the results match except (a) where a cumulative probability lies within
+    float rounding of 1 - top_p (the two sums add in different orders) and
+    (b) in the order of equal candidates.
+
+    Returns (warped scores, overflow): overflow is a 0-d bool tensor that is
+    True when a row may hold more values tied with the k-th largest than the
+    candidate set has room for; the caller then uses `warp`."""
+    k = max(TOP_K, keep)
+    vocab = scores.shape[-1]
+    if k > vocab:  # the reference's top-k rejects it: same error
+        return warp(scores, temperature, top_p, keep), torch.zeros((), dtype=torch.bool)
+    if temperature != 1.0:
+        scores = scores / temperature
+    kc = min(k + TIE_ROOM, vocab)
+    values, index = torch.topk(scores, kc)  # descending
+    threshold = values[..., k - 1:k]
+    values = values.masked_fill(values < threshold, float("-inf"))
+    if kc < vocab:
+        overflow = (values[..., -1] == threshold[..., 0]).any()
+    else:
+        overflow = torch.zeros((), dtype=torch.bool, device=scores.device)
+    if top_p < 1.0:
+        ascending = values.flip(-1)
+        remove = ascending.softmax(-1).cumsum(-1) <= 1 - top_p
+        remove[..., -keep:] = False
+        values = values.masked_fill(remove.flip(-1), float("-inf"))
+    out = torch.full_like(scores, float("-inf")).scatter_(-1, index, values)
+    return out, overflow
+
+
 def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, capacity=None,
                on_prefill=None, on_step=None):
     """Beam sampling (runtime_shared.py:214-265) for a fixed number of decode
     steps: every step samples 2 * beams continuations from all beams, keeps
-    the best `beams`, reorders the cache and decodes. End-of-sequence tokens
+    the best `beams`, reorders the cache and decodes. The warpers run on each
+    row's top-k candidates (`warp_candidates`), or on the whole vocabulary
+    (`warp`) when ties at the top-k threshold overflow the candidate set. End-of-sequence tokens
     do not stop it, so every call performs exactly `steps` decode steps.
     `on_prefill()` runs after the prefill and `on_step(i)` after decode step i.
     Returns (best token sequence, per-step running scores)."""
@@ -362,10 +406,19 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
     running_scores = [0.0] + [-1e9] * (beams - 1)
     seen = torch.zeros((beams, vocab), dtype=torch.bool, device=device)
     for step in range(steps):
-        log_probs = warp(penalize(torch.log_softmax(logits.float(), -1), seen), temperature, top_p, 2)
-        scores = (log_probs + torch.tensor(running_scores, device=device)[:, None]).view(1, -1)
+        penalized = penalize(torch.log_softmax(logits.float(), -1), seen)
+        running_t = torch.tensor(running_scores, device=device)[:, None]
+        log_probs, overflow = warp_candidates(penalized, temperature, top_p, 2)
+        scores = (log_probs + running_t).view(1, -1)
         probs = scores.softmax(-1)
-        picks = torch.multinomial(probs, min(keep, int(torch.count_nonzero(probs))))
+        # One host read for the sample count and the tie check.
+        possible, overflow = torch.stack((torch.count_nonzero(probs), overflow.long())).tolist()
+        if overflow:
+            log_probs = warp(penalized, temperature, top_p, 2)
+            scores = (log_probs + running_t).view(1, -1)
+            probs = scores.softmax(-1)
+            possible = int(torch.count_nonzero(probs))
+        picks = torch.multinomial(probs, min(keep, possible))
         picked = scores.gather(1, picks)[0].tolist()
         parents, tokens = zip(*(divmod(pick, vocab) for pick in picks[0].tolist()))
         order = sorted(range(len(picked)), key=picked.__getitem__, reverse=True)[:beams]
