@@ -209,11 +209,13 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   // Automatic choice (measured at the StarCoder2-8B and GPTBigCode-1B shapes):
   // the matrix-core path wins for Q5_0 at every M and for Q4_0 / Q8_0 from
   // M = 2; at M = 1 the vector path's dot products are cheap enough, except
-  // on matrices of 32 MiB or less, where the shorter prologue of this kernel
-  // wins (4608 x 4608 and 5632 x 4608).
+  // on matrices of 32 MiB or less with K = 4608 (4608 x 4608 and 5632 x
+  // 4608), or up to K = 8192 for Q8_0 (8192 x 2048).
   const uint64_t q_bytes = (uint64_t)n * (k / 32) * payload_bytes(qtype);
-  if (tu.path == 0 && qtype != SVQ_Q5_0 && m < 2 && (q_bytes > (32u << 20) || k > 8192))
-    return false;
+  if (tu.path == 0 && qtype != SVQ_Q5_0 && m < 2) {
+    const bool k_ok = qtype == SVQ_Q8_0 ? k <= 8192 : (k >= 4096 && k <= 6144);
+    if (q_bytes > (32u << 20) || !k_ok) return false;
+  }
   if (q_bytes >= (1ull << 31) || (uint64_t)n * (k / 16) >= (1ull << 31)) return false;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
