@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -144,6 +145,16 @@ constexpr size_t kStreamLdsMax = 156 * 1024;  // nearly all of a CU's 160 KB
 // exactly this many per CU.
 constexpr int kPersistentGroupsPerCu = 2;
 
+// Workgroups of a persistent launch that needs `want` of them (one tile
+// group each): a whole number of workgroups per CU, at most
+// kPersistentGroupsPerCu, so that wave-major tile numbering loads every CU
+// alike; never more than the `cap` the GPU keeps resident.
+int balanced_groups(int want, int cus, int cap) {
+  const int per_cu = std::min((want + cus - 1) / cus, kPersistentGroupsPerCu);
+  const int groups = per_cu * cus;
+  return groups <= cap ? groups : std::min(want, cap);
+}
+
 // Streaming launch: lanes per row and rows per lane group chosen so that the
 // row tiles cover every resident wave (largest tiles first, which reuse x
 // the most); when there are more tiles than resident waves, the wave count is
@@ -195,7 +206,7 @@ bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out
   *rows_out = rows;
   *wpg_out = wpg;
   *waves_out = waves;
-  *groups_out = (waves + wpg - 1) / wpg;
+  *groups_out = balanced_groups((waves + wpg - 1) / wpg, cus, wmax / wpg);
   if (wmax_out) *wmax_out = wmax;
   return true;
 }
@@ -273,11 +284,13 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   int groups = tile_groups < cap ? tile_groups : cap;
   const int rounds = (tile_groups + groups - 1) / groups;
   groups = (tile_groups + rounds - 1) / rounds;
-  // More tile groups than two workgroups per CU: exactly two per CU, which
-  // streams faster than filling every resident slot (measured 5-18% on the
-  // 8B c_fc and lm_head shapes at M = 1..4) and keeps the CUs evenly loaded.
-  if (tile_groups > kPersistentGroupsPerCu * cus && kPersistentGroupsPerCu * cus <= cap)
-    groups = kPersistentGroupsPerCu * cus;
+  // Without split K (wave-major tiles, one tile or none per wave when the
+  // matrix is short) the workgroup count is a whole number of workgroups per
+  // CU, at most two, so that every CU holds as many tiles as the next: two
+  // per CU streams faster than filling every resident slot (measured 5-18%
+  // on the 8B c_fc and lm_head shapes at M = 1..4), and rounding short
+  // matrices up to whole CUs 3-12% on qkv and o_proj.
+  if (ksplit == 1) groups = balanced_groups(tile_groups, cus, cap);
   *rows_out = rows;
   *ksplit_out = ksplit;
   *groups_out = groups;

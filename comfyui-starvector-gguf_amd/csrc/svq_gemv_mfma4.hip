@@ -101,20 +101,36 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   const int ri = lane & 3;     // row of the row set; also the A row it supplies
   const int m_a = ri % M;      // activation row it supplies (rows >= M repeat)
   // Work split: the WPG waves of a workgroup are P tile slots x S K-ranges;
-  // workgroup g processes tile groups g, g + G, ... (P tiles each), and wave
-  // (p, sk) streams steps [st0, st1) of tile p of each group. With S > 1 the
-  // S partial sums of a tile meet in LDS at the end of its group.
+  // wave (p, sk) streams steps [st0, st1) of each tile of slot p. With S > 1
+  // workgroup g processes tile groups g, g + G, ... (P tiles each) and the S
+  // partial sums of a tile meet in LDS at the end of its group.
   const int S = a.ksplit, P = WPG / S;
   const int p_id = wave / S, sk = wave % S;
   const int tile_rows = 4 * R;
   const int tiles = (n + tile_rows - 1) / tile_rows;
   const int groups = (tiles + P - 1) / P;
   const int G = gridDim.x;
-  const int my_tiles = (int)blockIdx.x < groups ? (groups - (int)blockIdx.x + G - 1) / G : 0;
+  // At most one tile per wave (S = 1): wave-major tiles (wave p of
+  // workgroup g owns tile wv = p * G + g), which spreads the idle waves of a
+  // short matrix over all workgroups, hence over all CUs. Otherwise workgroup
+  // g walks tile groups g, g + G, ... (P consecutive tiles each), which keeps
+  // the rows a workgroup streams at a time together; with S > 1 the S waves
+  // of a tile slot meet at a barrier per tile, so every wave of a workgroup
+  // walks the same number of tile groups.
+  const int WV = P * G;
+  const bool wave_major = S == 1 && tiles <= WV;
+  const int wv = p_id * G + (int)blockIdx.x;
+  const int my_tiles = wave_major
+                           ? (wv < tiles ? 1 : 0)
+                           : ((int)blockIdx.x < groups ? (groups - (int)blockIdx.x + G - 1) / G : 0);
   const int niter_all = (units + kSlots * U - 1) / (kSlots * U);
   const int st0 = sk * niter_all / S, st1 = (sk + 1) * niter_all / S;
   const int steps = my_tiles * (st1 - st0);
-  auto tile_of = [&](int j) { return ((int)blockIdx.x + j * G) * P + p_id; };
+  auto tile_of = [&](int j) { return wave_major ? wv + j * WV : ((int)blockIdx.x + j * G) * P + p_id; };
+  // A workgroup without tiles leaves before staging x (the same decision for
+  // all its waves): wave-major, when its first wave (wv = g) has none;
+  // otherwise when it has no tile group.
+  if ((int)blockIdx.x >= (wave_major ? tiles : groups)) return;
   const uint32_t row_bytes = (uint32_t)kb * T::kBlockQ;
 
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)n * row_bytes);

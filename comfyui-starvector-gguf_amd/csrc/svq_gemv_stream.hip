@@ -6,11 +6,14 @@
 // scaled by the block's fp16 scale once; bias added in fp32; fp16 or fp32 out.
 //
 // Work mapping:
-//   * The grid holds only as many waves as the GPU keeps resident (W, from
-//     the occupancy of this kernel). Each workgroup of 4 waves stages x and
-//     the per-unit offset sums into LDS once, before its first weight load,
-//     and then every wave streams its own rows to the end of the matrix. A wave owns row tiles
-//     t = wave, wave + W, wave + 2W, ...; a tile is (64 / G) * R rows: G lanes
+//   * The grid holds at most as many waves as the GPU keeps resident (W, from
+//     the occupancy of this kernel, and at most two workgroups per CU). Each
+//     workgroup of 4 waves stages x and the per-unit offset sums into LDS
+//     once, before its first weight load, and then every wave streams its own
+//     rows to the end of the matrix. Wave w of workgroup b is wave
+//     wid = b * 4 + w of the grid (wid = w * B + b with B workgroups when
+//     there is at most one tile per wave) and owns row tiles
+//     t = wid, wid + W, wid + 2W, ...; a tile is (64 / G) * R rows: G lanes
 //     share a row and stride over its units, R rows per lane group reuse each
 //     activation read from LDS.
 //   * A wave's work is one flat sequence of steps (tile, unit-iteration). A
@@ -58,10 +61,19 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   const int tile_rows = (64 >> lg_g) * R;
   const int tiles = (n + tile_rows - 1) / tile_rows;
   const int W = a.waves;
-  const int wid = blockIdx.x * WPG + wave;
+  // At most one tile per wave: wave-major numbering (wave w of workgroup b
+  // is wid = w * gridDim.x + b), which spreads the idle waves of a short
+  // matrix over all workgroups, hence over all CUs. Otherwise wid =
+  // b * WPG + w: the waves of a workgroup stream neighbouring tiles.
+  const bool wave_major = tiles <= W;
+  const int wid = wave_major ? wave * (int)gridDim.x + (int)blockIdx.x
+                             : (int)blockIdx.x * WPG + wave;
   const int my_tiles = wid < W ? (tiles - wid + W - 1) / W : 0;
   const int niter = (units + G - 1) >> lg_g;  // unit iterations per tile
   const int steps = my_tiles * niter;
+  // A workgroup without tiles leaves before staging x (the same decision for
+  // all its waves): its lowest wave number is b (wave-major) or b * WPG.
+  if ((wave_major ? (int)blockIdx.x : (int)blockIdx.x * WPG) >= min(W, tiles)) return;
   const uint32_t row_bytes = (uint32_t)kb * T::kBlockQ;
 
   // Buffer resources over the whole arrays (the C ABI keeps them < 2^31
