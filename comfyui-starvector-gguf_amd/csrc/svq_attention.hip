@@ -139,32 +139,17 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
   const int heads = a.kv_heads * G;
   const bool rope = a.cos != nullptr;
 
-  // Rotation of a lane's 4 pieces (dims 32 ks + 8g): the partner of piece ks
-  // is piece ks ^ 2 (dims + 64 mod 128); the lower half of the dims is ks < 2.
-  auto rotate4 = [&](u32x4 (&v)[4]) {
-    if (!rope) return;
-    u32x4 r[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int d = 32 * ks + 8 * g;
-      r[ks] = rope8(v[ks], v[ks ^ 2], load16(a.cos + d), load16(a.sin + d), ks < 2);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) v[ks] = r[ks];
-  };
-
+  // The loads go out in the order their data is needed, before any of it is
+  // used (vector loads retire in issue order): q, the new key and value, the
+  // rotation tables, then the chunk's keys and values. The rotations then
+  // wait only for the first group, while the chunk loads are in flight.
   // Q^T (B of the score MFMAs): query head kv * G + n, zero for n >= G.
   const uint16_t* qrow = a.qkv + (int64_t)row * a.qkv_stride;
   u32x4 qb[4];
   const uint16_t* qh = qrow + (kv * G + (n < G ? n : 0)) * kD;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) qb[ks] = load16(qh + 32 * ks + 8 * g);
-  rotate4(qb);
-  if (n >= G) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qb[ks] = u32x4{0, 0, 0, 0};
-  }
-  // The new key (rotated) and value at this lane's dims.
+  // The new key (rotated below) and value at this lane's dims.
   u32x4 kn[4], vn[4];
   const uint16_t* krow = qrow + (heads + kv) * kD;
   const uint16_t* vrow = qrow + (heads + a.kv_heads + kv) * kD;
@@ -173,7 +158,15 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
     kn[ks] = load16(krow + 32 * ks + 8 * g);
     vn[ks] = load16(vrow + 32 * ks + 8 * g);
   }
-  rotate4(kn);
+  // Rotation tables at the lane's dims 32 ks + 8g.
+  u32x4 cs[4], sn[4];
+  if (rope) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      cs[ks] = load16(a.cos + 32 * ks + 8 * g);
+      sn[ks] = load16(a.sin + 32 * ks + 8 * g);
+    }
+  }
 
   const int64_t slab = (int64_t)rk * a.capacity * kD;
   uint16_t* kslab = a.keys + slab;
@@ -182,15 +175,30 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
   const __amdgpu_buffer_rsrc_t kr = make_rsrc(kslab, (uint32_t)a.span * kD * 2);
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(vslab, (uint32_t)a.span * kD * 2);
 
+  // Bias of the lane's two key/value slots s0 + 16t + n (bkv) and of its
+  // eight score slots s0 + 16t + 4g + i (bsc); -inf past the span.
+  float bkv[2], bsc[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int j = s0 + 16 * t + n;
+    bkv[t] = j >= a.span ? -INFINITY : a.bias ? half_bits_to_float(a.bias[j]) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int js = s0 + 16 * t + 4 * g + i;
+      bsc[t][i] = js >= a.span ? -INFINITY : a.bias ? half_bits_to_float(a.bias[js]) : 0.0f;
+    }
+  }
+
   // K (A of the score MFMAs) and V (staged to LDS) of slot s0 + 16t + n.
-  // Masked slots (past the span or with a -inf bias) and the new slot load
-  // nothing; the new slot takes kn / vn and is written to the cache.
+  // Slots before the position (every slot of the span without a bias) are
+  // loaded without waiting for their bias; slots past the position, which a
+  // decode step's bias masks, are loaded below only if their bias does not.
+  // The new slot takes kn / vn and is written to the cache.
   u32x4 ka[2][4], va[2][4];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int j = s0 + 16 * t + n;
-    bool load = j < a.span && j != pos;
-    if (load && a.bias) load = half_bits_to_float(a.bias[j]) != -INFINITY;
+    const bool load = j < a.span && j != pos && (a.bias == nullptr || j < pos);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const uint32_t off = load ? (uint32_t)j * kD * 2 + (32u * ks + 8u * g) * 2 : kOutOfRange;
@@ -198,6 +206,37 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
       va[t][ks] = __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0);
     }
   }
+  if (a.bias) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int j = s0 + 16 * t + n;
+      if (j > pos && bkv[t] != -INFINITY) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const uint32_t off = (uint32_t)j * kD * 2 + (32u * ks + 8u * g) * 2;
+          ka[t][ks] = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
+          va[t][ks] = __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0);
+        }
+      }
+    }
+  }
+
+  // Rotation of a lane's 4 pieces (dims 32 ks + 8g): the partner of piece ks
+  // is piece ks ^ 2 (dims + 64 mod 128); the lower half of the dims is ks < 2.
+  auto rotate4 = [&](u32x4 (&v)[4]) {
+    if (!rope) return;
+    u32x4 r[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) r[ks] = rope8(v[ks], v[ks ^ 2], cs[ks], sn[ks], ks < 2);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) v[ks] = r[ks];
+  };
+  rotate4(qb);
+  if (n >= G) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qb[ks] = u32x4{0, 0, 0, 0};
+  }
+  rotate4(kn);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int j = s0 + 16 * t + n;
@@ -209,6 +248,10 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
         *reinterpret_cast<u32x4*>(kslab + pos * kD + 32 * ks + 8 * g) = kn[ks];
         *reinterpret_cast<u32x4*>(vslab + pos * kD + 32 * ks + 8 * g) = vn[ks];
       }
+    }
+    if (bkv[t] == -INFINITY) {  // masked: its probability is 0, its V must be finite
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) va[t][ks] = u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) vst[(w * 32 + 16 * t + n) * kVRow + 4 * ks + g] = va[t][ks];
@@ -224,9 +267,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
     for (int ks = 0; ks < 4; ++ks) d = mfma16x16x32(ka[t][ks], qb[ks], d);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int j = s0 + 16 * t + 4 * g + i;
-      float b = -INFINITY;
-      if (j < a.span) b = a.bias ? half_bits_to_float(a.bias[j]) : 0.0f;
+      const float b = bsc[t][i];
       sc[t][i] = b == -INFINITY ? -INFINITY : (float)(_Float16)(fmaf(a.scale, d[i], b));
     }
   }

@@ -46,6 +46,8 @@ def make_case(rows, heads, kvh, capacity, span, position, rope=True, window=None
     slots = torch.arange(span)
     if bias_kind is None:
         bias = None
+    elif bias_kind == "zeros":
+        bias = torch.zeros(span).half()
     else:
         hidden = slots > position
         if window is not None:
@@ -128,6 +130,8 @@ CASES = [
     (2, 16, 1, 600, 512, 300, False, None, "causal"),     # GPTBigCode-1B multi-query
     (2, 8, 8, 100, 77, 76, True, None, None),             # one query head per kv head, no bias
     (2, 8, 2, 100, 33, 10, True, None, None),             # no bias: slots past position attended
+    (2, 8, 2, 300, 290, 100, True, None, "zeros"),        # zero bias: slots past position attended
+    (2, 36, 4, 600, 512, 450, True, 100, "causal"),       # window: masked slots before position
 ]
 
 
