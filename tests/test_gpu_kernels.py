@@ -201,6 +201,19 @@ def decoder_cases():
     return cases
 
 
+@pytest.mark.parametrize("qtype,n,k,m,has_bias", decoder_cases())
+def test_gemv_persistent_launch_shape(cuda_device, qtype, n, k, m, has_bias):
+    """Automatic streaming launches (both persistent kernels, no split K) use
+    a whole number of workgroups per CU, at most two: every CU holds the
+    same share of tiles."""
+    plan = native.gemv_plan(m, n, k, qtype)
+    if plan["kernel"] not in ("stream", "mfma4") or (plan["kernel"] == "mfma4" and plan["lg_g"] > 1):
+        return
+    cus = torch.cuda.get_device_properties(cuda_device).multi_processor_count
+    say(f"launch shape {qtype} m={m} n={n} k={k} plan={plan} cus={cus}")
+    assert plan["groups"] % cus == 0 and plan["groups"] <= 2 * cus, plan
+
+
 @pytest.mark.parametrize("kernel_path", ["auto", "mfma", "mfma4"], indirect=True)
 @pytest.mark.parametrize("qtype,n,k,m,has_bias", decoder_cases())
 def test_gemv_decoder_shapes(cuda_device, kernel_path, qtype, n, k, m, has_bias):
