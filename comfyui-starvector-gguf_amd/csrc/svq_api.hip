@@ -216,11 +216,12 @@ constexpr int kMfmaMinRows = 5;  // smallest M sent to the MFMA kernel by defaul
 // Streaming MFMA launch (M <= 4): row tiles of 4 rows (8 with two row sets
 // per lane) over 16 unit slots. Variant (the `rows` code): 3 = consecutive
 // units per lane (three Q4_0 / Q5_0 blocks, needs units % 48 == 0; one Q8_0
-// block), 2 = two row sets per lane, 1 = one. The 4 waves of a workgroup split K (S = 2 or 4) and add
-// their partial sums through LDS: by default S = 2 when single-row-set tiles
-// fill a quarter of the resident waves or fewer, otherwise as SVQ_MFMA_S asks. Workgroups are
-// persistent over tile groups, trimmed so that each processes the same number
-// of groups.
+// block), 2 = two row sets per lane, 1 = one. The 4 waves of a workgroup
+// split K (S = 2 or 4) and add their partial sums through LDS: by default
+// S = 2 when single-row-set tiles fill a quarter of the resident waves or
+// fewer, and for long Q8_0 rows; otherwise as SVQ_MFMA_S asks. Workgroups
+// are persistent over tile groups; without split K their count is a whole
+// number per CU, at most two (balanced_groups).
 bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_out,
                   int* ksplit_out, int* groups_out, int* wmax_out, size_t extra_lds = 0) {
   if ((tu.path != 4 && tu.path != 0) || m > 4) return false;
