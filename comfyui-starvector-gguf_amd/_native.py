@@ -66,6 +66,8 @@ def load() -> ctypes.CDLL:
         lib.svq_decode_attention.argtypes = [vp, i64, vp, vp, vp, vp, i64, vp, vp, i32, vp,
                                              i32, i32, i32, i32, ctypes.c_float, vp, i64, vp]
         lib.svq_decode_attention.restype = i32
+        lib.svq_cache_reorder.argtypes = [vp, i64, i32, i32, i64, i32, i64, vp, vp]
+        lib.svq_cache_reorder.restype = i32
         cp = ctypes.c_char_p
         lib.svq_gguf_open.argtypes = [cp, i32, ctypes.POINTER(vp)]
         lib.svq_gguf_open.restype = i32
@@ -268,6 +270,25 @@ def decode_attention(qkv: torch.Tensor, cos: torch.Tensor | None, sin: torch.Ten
             out.data_ptr(), rows, heads, kv_heads, head_dim, scale, workspace.data_ptr(),
             workspace.numel(), _stream(qkv.device))
     _check(lib, "svq_decode_attention", rc)
+
+
+def cache_reorder(cache: torch.Tensor, parents: torch.Tensor, length: int) -> None:
+    """Beam reorder of a contiguous fp16 cache [planes, rows, heads, capacity,
+    128] (svq_cache_reorder): row r takes the first `length` slots of row
+    parents[r] (a device int64 [rows] tensor) wherever the two differ."""
+    lib = load()
+    if cache.dim() != 5 or not cache.is_contiguous() or cache.dtype != torch.float16:
+        raise ValueError("cache must be a contiguous float16 [planes, rows, heads, capacity, "
+                         "head_dim] tensor")
+    planes, rows, heads, capacity, head_dim = cache.shape
+    if parents.dtype != torch.int64 or parents.shape != (rows,) or not parents.is_contiguous():
+        raise ValueError("parents must be a contiguous int64 tensor of one entry per row")
+    if parents.device != cache.device:
+        raise ValueError("cache and parents must be on one device")
+    with _on_device(cache.device):
+        rc = lib.svq_cache_reorder(cache.data_ptr(), planes, rows, heads, capacity, head_dim,
+                                   int(length), parents.data_ptr(), _stream(cache.device))
+    _check(lib, "svq_cache_reorder", rc)
 
 
 def pack_soa(aos_ptr: int, nblocks: int, qtype: str, q: torch.Tensor, s: torch.Tensor,

@@ -601,4 +601,25 @@ int svq_decode_attention(const uint16_t* qkv, int64_t qkv_stride, const uint16_t
   return 0;
 }
 
+int svq_cache_reorder(uint16_t* cache, int64_t planes, int rows, int heads, int64_t capacity,
+                      int head_dim, int64_t length, const int64_t* parents, void* stream) {
+  if (planes < 1 || rows < 1 || rows > SVQ_MAX_ROWS || heads < 1 || head_dim != SVQ_HEAD_DIM ||
+      length < 0 || capacity < length || capacity < 1 || planes * heads > 65535)
+    return fail(SVQ_E_SHAPE,
+                "invalid cache shape planes=%lld rows=%d heads=%d capacity=%lld head_dim=%d "
+                "length=%lld",
+                (long long)planes, rows, heads, (long long)capacity, head_dim,
+                (long long)length);
+  if (length * (head_dim / 8) / 256 >= ((int64_t)1 << 31))
+    return fail(SVQ_E_RANGE, "cache reorder length too large");
+  if (!cache || !parents) return fail(SVQ_E_NULL, "NULL cache or parents");
+  if (!aligned(cache, 16) || !aligned(parents, 8))
+    return fail(SVQ_E_ALIGN, "misaligned cache or parents");
+  if (length == 0) return 0;
+  svq::ReorderArgs a{cache, capacity, length, parents, rows, heads};
+  const hipError_t e = svq::launch_cache_reorder(a, planes, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "svq_cache_reorder launch");
+  return 0;
+}
+
 }  // extern "C"

@@ -423,6 +423,40 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnMerge a) {
   }
 }
 
+// Beam reorder (the cache copies of runtime_shared.py:388-394): every row r
+// whose parent p = parents[r] differs from r takes the first `length` slots
+// of each (plane, head) of row p. A thread owns one 16-byte piece position
+// of one (plane, head) and moves it for every row, reading all sources
+// before it writes, so rows that exchange caches need no staging copy. A
+// parent outside [0, rows) leaves its row as it is.
+constexpr int kReorderMaxRows = 8;
+
+__global__ __launch_bounds__(256) void cache_reorder_kernel(ReorderArgs a) {
+  const int64_t pieces = a.length * (kD / 8);  // 16-byte pieces per (plane, row, head)
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= pieces) return;
+  const int64_t ph = blockIdx.y;  // plane * heads + head
+  const int64_t plane = ph / a.heads, head = ph - plane * a.heads;
+  const int64_t head_pieces = a.capacity * (kD / 8);
+  const int64_t row_pieces = (int64_t)a.heads * head_pieces;
+  u32x4* base = reinterpret_cast<u32x4*>(a.cache) + plane * a.rows * row_pieces +
+                head * head_pieces + e;
+  int par[kReorderMaxRows];
+  u32x4 v[kReorderMaxRows];
+#pragma unroll
+  for (int r = 0; r < kReorderMaxRows; ++r) {
+    par[r] = r;
+    if (r < a.rows) {
+      const int64_t p = a.parents[r];
+      if (p >= 0 && p < a.rows) par[r] = (int)p;
+    }
+    if (par[r] != r) v[r] = base[par[r] * row_pieces];
+  }
+#pragma unroll
+  for (int r = 0; r < kReorderMaxRows; ++r)
+    if (par[r] != r) base[r * row_pieces] = v[r];
+}
+
 template <int G>
 hipError_t launch_g(const AttnArgs& a, int rows, hipStream_t stream) {
   const dim3 grid(a.nchunks, rows * a.kv_heads);
@@ -450,6 +484,13 @@ hipError_t launch_decode_attention(const AttnArgs& a, int rows, int group, hipSt
   AttnMerge m{a.ml, a.acc, a.out, a.nchunks};
   hipLaunchKernelGGL(merge_kernel, dim3(rows * a.kv_heads * group), dim3(256),
                      a.nchunks * sizeof(float), stream, m);
+  return hipGetLastError();
+}
+
+hipError_t launch_cache_reorder(const ReorderArgs& a, int64_t planes, hipStream_t stream) {
+  const int64_t pieces = a.length * (kD / 8);
+  const dim3 grid((unsigned)((pieces + 255) / 256), (unsigned)(planes * a.heads));
+  hipLaunchKernelGGL(cache_reorder_kernel, grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -101,6 +101,16 @@ int64_t attention_ml_bytes(int rows, int heads, int span);
 hipError_t launch_chunks(const AttnArgs& a, int rows, int group, hipStream_t stream);
 int64_t attention_workspace_bytes(int rows, int heads, int kv_heads, int span);
 hipError_t launch_decode_attention(const AttnArgs& a, int rows, int group, hipStream_t stream);
+// Beam reorder of a [planes, rows, heads, capacity, 128] fp16 cache.
+struct ReorderArgs {
+  uint16_t* cache;
+  int64_t capacity;          // slots per (plane, row, head)
+  int64_t length;            // leading slots moved
+  const int64_t* parents;    // device int64 [rows]
+  int rows;
+  int heads;
+};
+hipError_t launch_cache_reorder(const ReorderArgs& a, int64_t planes, hipStream_t stream);
 
 hipError_t launch_dequant(const uint8_t* q, const uint16_t* s, void* out,
                           int64_t nblocks, int qtype, int out_dtype,

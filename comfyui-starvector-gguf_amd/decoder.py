@@ -323,6 +323,17 @@ class CachedDecoding:
             for cache in (self.keys, self.values):
                 cache[:, row, :, :n].copy_(cache[:, parent, :, :n])
 
+    def reorder_rows(self, parents):
+        """`reorder` with the parents as a device int64 tensor [rows]: on the
+        GPU one kernel per cache (svq_cache_reorder) moves the rows whose parent
+        differs, with no host round trip; on the host it reads the parents and
+        calls `reorder`."""
+        if self.keys.is_cuda:
+            for cache in (self.keys, self.values):
+                native.cache_reorder(cache, parents, self.length)
+        else:
+            self.reorder(parents.tolist())
+
 
 def penalize(scores, seen):
     """Repetition penalty over generated tokens (runtime_shared.py:170-173)."""
@@ -392,9 +403,18 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
     steps: every step samples 2 * beams continuations from all beams, keeps
     the best `beams`, reorders the cache and decodes. The warpers run on each
     row's top-k candidates (`warp_candidates`), or on the whole vocabulary
-    (`warp`) when ties at the top-k threshold overflow the candidate set. End-of-sequence tokens
-    do not stop it, so every call performs exactly `steps` decode steps.
-    `on_prefill()` runs after the prefill and `on_step(i)` after decode step i.
+    (`warp`) when ties at the top-k threshold overflow the candidate set.
+    End-of-sequence tokens do not stop it, so every call performs exactly
+    `steps` decode steps. `on_prefill()` runs after the prefill and
+    `on_step(i)` after decode step i.
+
+    The selection of the surviving beams (the reference's sort of the picked
+    scores, descending and stable) stays on the device: parents, tokens and
+    running scores are device tensors that feed the cache reorder, the
+    seen-token mask and the next step directly, so a step reads back only the
+    number of possible samples (`count_nonzero`, which the reference also
+    reads before sampling). The token sequences are rebuilt from the
+    per-step parents and tokens at the end.
     Returns (best token sequence, per-step running scores)."""
     keep = 2 * beams
     capacity = capacity or embeddings.shape[1] + steps + 1
@@ -402,35 +422,47 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
     if on_prefill is not None:
         on_prefill()
     device, vocab = logits.device, logits.shape[-1]
-    running = [[] for _ in range(beams)]
-    running_scores = [0.0] + [-1e9] * (beams - 1)
+    running_t = torch.tensor([0.0] + [-1e9] * (beams - 1), device=device)
     seen = torch.zeros((beams, vocab), dtype=torch.bool, device=device)
+    beam_index = torch.arange(beams, device=device)
+    history = []
     for step in range(steps):
         penalized = penalize(torch.log_softmax(logits.float(), -1), seen)
-        running_t = torch.tensor(running_scores, device=device)[:, None]
         log_probs, overflow = warp_candidates(penalized, temperature, top_p, 2)
-        scores = (log_probs + running_t).view(1, -1)
+        scores = (log_probs + running_t[:, None]).view(1, -1)
         probs = scores.softmax(-1)
         # One host read for the sample count and the tie check.
         possible, overflow = torch.stack((torch.count_nonzero(probs), overflow.long())).tolist()
         if overflow:
             log_probs = warp(penalized, temperature, top_p, 2)
-            scores = (log_probs + running_t).view(1, -1)
+            scores = (log_probs + running_t[:, None]).view(1, -1)
             probs = scores.softmax(-1)
             possible = int(torch.count_nonzero(probs))
-        picks = torch.multinomial(probs, min(keep, possible))
-        picked = scores.gather(1, picks)[0].tolist()
-        parents, tokens = zip(*(divmod(pick, vocab) for pick in picks[0].tolist()))
-        order = sorted(range(len(picked)), key=picked.__getitem__, reverse=True)[:beams]
-        running_scores = [picked[j] for j in order] + [-1e9] * (beams - len(order))
-        order += [order[0]] * (beams - len(order))
-        running = [running[parents[j]] + [tokens[j]] for j in order]
-        selected = torch.tensor([parents[j] for j in order], device=device)
-        next_tokens = torch.tensor([tokens[j] for j in order], device=device)
-        seen = seen[selected]
-        seen[torch.arange(beams, device=device), next_tokens] = True
-        decoding.reorder([parents[j] for j in order])
-        logits = decoding.step(next_tokens)
+        picks = torch.multinomial(probs, min(keep, possible))[0]
+        picked = scores[0].gather(0, picks)
+        # sorted(range(n), key=picked, reverse=True)[:beams]: descending, stable.
+        ordered, order = torch.sort(picked, descending=True, stable=True)
+        kept = min(beams, picks.numel())
+        chosen = picks[order[:kept]]
+        running_t = ordered[:kept]
+        if kept < beams:  # the reference repeats its best pick and scores the rest -1e9
+            chosen = torch.cat((chosen, chosen[:1].expand(beams - kept)))
+            running_t = torch.cat((running_t, torch.full((beams - kept,), -1e9, device=device)))
+        parents, tokens = chosen // vocab, chosen % vocab
+        history.append((parents, tokens))
+        seen = seen[parents]
+        seen[beam_index, tokens] = True
+        decoding.reorder_rows(parents)
+        logits = decoding.step(tokens)
         if on_step is not None:
             on_step(step + 1)
-    return running[0], running_scores
+    # The token sequences: follow each final beam back through its parents.
+    if not history:
+        return [], running_t.tolist()
+    parents_all = torch.stack([p for p, _ in history]).tolist()
+    tokens_all = torch.stack([t for _, t in history]).tolist()
+    beam, best = 0, []
+    for step in range(len(history) - 1, -1, -1):
+        best.append(tokens_all[step][beam])
+        beam = parents_all[step][beam]
+    return best[::-1], running_t.tolist()

@@ -182,6 +182,23 @@ int svq_decode_attention(const uint16_t *qkv, int64_t qkv_stride, const uint16_t
                          int64_t workspace_bytes, void *stream);
 
 /*
+ * Beam reorder of a decode cache, fused over rows: every row r whose parent
+ * p = parents[r] differs from r takes the first `length` slots of every
+ * (plane, head) of row p; rows may exchange caches (all sources are read
+ * before any row is written). Replaces CachedDecoding.reorder
+ * (runtime_shared.py:388-394), whose parents come from the host; here they
+ * are a device array, so a beam step needs no host round trip.
+ *   cache    fp16 [planes, rows, heads, capacity, head_dim] contiguous
+ *            (16-byte aligned), e.g. every layer's keys at once
+ *   parents  device int64 [rows]; a value outside [0, rows) leaves its row
+ *            unchanged
+ * rows <= SVQ_MAX_ROWS, head_dim == SVQ_HEAD_DIM, length <= capacity,
+ * planes * heads <= 65535.
+ */
+int svq_cache_reorder(uint16_t *cache, int64_t planes, int rows, int heads, int64_t capacity,
+                      int head_dim, int64_t length, const int64_t *parents, void *stream);
+
+/*
  * GGUF container reader (host memory; no GPU needed). Replaces the PyPI
  * `gguf` GGUFReader the reference opens its checkpoints with
  * (gguf_support.py:101-121): GGUF versions 2 and 3, memory-mapped once,

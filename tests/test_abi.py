@@ -150,6 +150,32 @@ def test_decode_attention_workspace_size():
     assert lib.svq_decode_attention_workspace(2, 34, 2, 64) == -2  # 17 heads per kv head
 
 
+def cache_reorder(**kw):
+    args = dict(cache=FAKE, planes=32, rows=2, heads=4, capacity=64, head_dim=128, length=10,
+                parents=FAKE)
+    args.update(kw)
+    return native.load().svq_cache_reorder(
+        args["cache"], args["planes"], args["rows"], args["heads"], args["capacity"],
+        args["head_dim"], args["length"], args["parents"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(rows=0), -2), (dict(rows=9), -2), (dict(planes=0), -2), (dict(heads=0), -2),
+    (dict(head_dim=64), -2), (dict(length=65), -2), (dict(length=-1), -2),
+    (dict(planes=70000, heads=1), -2),
+    (dict(cache=None), -3), (dict(parents=None), -3),
+    (dict(cache=FAKE + 8), -6), (dict(parents=FAKE + 4), -6),
+])
+def test_cache_reorder_rejects_bad_arguments(kw, code):
+    assert cache_reorder(**kw) == code
+    assert native.load().svq_last_error().decode()
+
+
+def test_cache_reorder_empty_length_is_a_no_op():
+    # Nothing to move: returns before any launch (no device needed).
+    assert cache_reorder(length=0) == 0
+
+
 def gemv_fused(**kw):
     args = dict(x=FAKE, q=FAKE, s=FAKE, bias=None, y=FAKE + 1024, m=2, n=8, k=64, qtype=4,
                 ln_w=None, ln_b=None, eps=1e-5, res=None, act=0)

@@ -188,3 +188,65 @@ def test_beam_steps_overflow_uses_warp(monkeypatch):
         tokens, _ = beam_steps(model, emb, 3, beams=2)
     assert len(tokens) == 3
     assert len(calls) == 3  # TIE_ROOM 0: the k-th value always fills the last slot
+
+
+def beam_steps_host_selection(decoder_model, embeddings, steps, beams=2, temperature=1.5,
+                              top_p=0.9):
+    """The beam loop with the survivors chosen on the host, as the reference
+    does (runtime_shared.py:214-265: Python lists, `sorted`, a host list of
+    parents for the cache reorder) -- the checker for `beam_steps`, whose
+    selection stays on the device."""
+    keep = 2 * beams
+    decoding, logits = decoder_model.prefill(embeddings, beams, embeddings.shape[1] + steps + 1)
+    device, vocab = logits.device, logits.shape[-1]
+    running = [[] for _ in range(beams)]
+    running_scores = [0.0] + [-1e9] * (beams - 1)
+    seen = torch.zeros((beams, vocab), dtype=torch.bool, device=device)
+    for _ in range(steps):
+        penalized = decoder.penalize(torch.log_softmax(logits.float(), -1), seen)
+        log_probs, overflow = decoder.warp_candidates(penalized, temperature, top_p, 2)
+        if bool(overflow):
+            log_probs = decoder.warp(penalized, temperature, top_p, 2)
+        scores = (log_probs + torch.tensor(running_scores, device=device)[:, None]).view(1, -1)
+        probs = scores.softmax(-1)
+        picks = torch.multinomial(probs, min(keep, int(torch.count_nonzero(probs))))
+        picked = scores.gather(1, picks)[0].tolist()
+        parents, tokens = zip(*(divmod(pick, vocab) for pick in picks[0].tolist()))
+        order = sorted(range(len(picked)), key=picked.__getitem__, reverse=True)[:beams]
+        running_scores = [picked[j] for j in order] + [-1e9] * (beams - len(order))
+        order += [order[0]] * (beams - len(order))
+        running = [running[parents[j]] + [tokens[j]] for j in order]
+        selected = torch.tensor([parents[j] for j in order], device=device)
+        next_tokens = torch.tensor([tokens[j] for j in order], device=device)
+        seen = seen[selected]
+        seen[torch.arange(beams, device=device), next_tokens] = True
+        decoding.reorder([parents[j] for j in order])
+        logits = decoding.step(next_tokens)
+    return running[0], running_scores
+
+
+def test_beam_steps_matches_host_selection_cpu():
+    """Device-side survivor selection and cache reorder give the sequence and
+    scores of the host-side bookkeeping (same seed, same draws)."""
+    model = small_model("cpu")
+    emb = prompt(5, "cpu", torch.float32)
+    with torch.inference_mode():
+        torch.manual_seed(4)
+        want = beam_steps_host_selection(model, emb, 6, beams=2)
+        torch.manual_seed(4)
+        got = beam_steps(model, emb, 6, beams=2)
+    assert got[0] == want[0] and got[1] == want[1], (got, want)
+
+
+@pytest.mark.gpu
+def test_beam_steps_matches_host_selection_gpu(cuda_device):
+    """The same on the GPU: the svq_cache_reorder kernel and graph-replayed
+    steps against host-chosen parents and torch slice copies."""
+    model = small_model(cuda_device)
+    emb = prompt(9, cuda_device, torch.float16)
+    with torch.inference_mode():
+        torch.manual_seed(5)
+        want = beam_steps_host_selection(model, emb, 8, beams=2)
+        torch.manual_seed(5)
+        got = beam_steps(model, emb, 8, beams=2)
+    assert got[0] == want[0] and got[1] == want[1], (got, want)

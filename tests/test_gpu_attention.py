@@ -214,3 +214,23 @@ def test_decode_attention_graph_replays(cuda_device):
         got = out.float().cpu()
         assert (got - ref).abs().max().item() <= 2e-3 * ref.abs().max().item(), p
         host_keys, host_values = rkeys, rvalues
+
+
+@pytest.mark.parametrize("rows,parents", [(2, (0, 1)), (2, (0, 0)), (2, (1, 1)), (2, (1, 0)),
+                                          (4, (2, 2, 0, 1)), (8, (7, 0, 1, 2, 3, 4, 5, 6)),
+                                          (3, (5, -1, 0))])
+def test_cache_reorder_matches_indexing(cuda_device, rows, parents):
+    """svq_cache_reorder against the reference's index copy (rows whose parent
+    differs take the parent's first `length` slots; rows may exchange
+    caches); parents outside [0, rows) leave their row unchanged."""
+    planes, heads, capacity, length = 3, 2, 40, 29
+    g = torch.Generator().manual_seed(rows)
+    cache = torch.randn(planes, rows, heads, capacity, HD, generator=g).half()
+    fixed = [p if 0 <= p < rows else r for r, p in enumerate(parents)]
+    want = cache.clone()
+    moved = [r for r, p in enumerate(fixed) if p != r]
+    if moved:
+        want[:, moved, :, :length] = cache[:, [fixed[r] for r in moved], :, :length]
+    got = cache.to(cuda_device)
+    native.cache_reorder(got, torch.tensor(parents, dtype=torch.int64, device=cuda_device), length)
+    assert torch.equal(got.cpu(), want)
