@@ -425,24 +425,23 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnMerge a) {
 
 // Beam reorder (the cache copies of runtime_shared.py:388-394): every row r
 // whose parent p = parents[r] differs from r takes the first `length` slots
-// of each (plane, head) of row p. A thread owns one 16-byte piece position
-// of one (plane, head) and moves it for every row, reading all sources
-// before it writes, so rows that exchange caches need no staging copy. A
-// parent outside [0, rows) leaves its row as it is.
+// of each (plane, head) of row p. A thread owns four 16-byte piece
+// positions (256 apart) of one (plane, head) and moves them for every row,
+// reading all sources before it writes, so rows that exchange caches need no
+// staging copy. A parent outside [0, rows) leaves its row as it is.
 constexpr int kReorderMaxRows = 8;
+constexpr int kReorderPieces = 4;  // 16-byte pieces per thread (256 threads apart)
 
 __global__ __launch_bounds__(256) void cache_reorder_kernel(ReorderArgs a) {
   const int64_t pieces = a.length * (kD / 8);  // 16-byte pieces per (plane, row, head)
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= pieces) return;
+  const int64_t e0 = (int64_t)blockIdx.x * 256 * kReorderPieces + threadIdx.x;
   const int64_t ph = blockIdx.y;  // plane * heads + head
   const int64_t plane = ph / a.heads, head = ph - plane * a.heads;
   const int64_t head_pieces = a.capacity * (kD / 8);
   const int64_t row_pieces = (int64_t)a.heads * head_pieces;
   u32x4* base = reinterpret_cast<u32x4*>(a.cache) + plane * a.rows * row_pieces +
-                head * head_pieces + e;
+                head * head_pieces;
   int par[kReorderMaxRows];
-  u32x4 v[kReorderMaxRows];
 #pragma unroll
   for (int r = 0; r < kReorderMaxRows; ++r) {
     par[r] = r;
@@ -450,11 +449,28 @@ __global__ __launch_bounds__(256) void cache_reorder_kernel(ReorderArgs a) {
       const int64_t p = a.parents[r];
       if (p >= 0 && p < a.rows) par[r] = (int)p;
     }
-    if (par[r] != r) v[r] = base[par[r] * row_pieces];
+  }
+  // Every source piece of this thread is read before any is written, so
+  // rows that exchange caches need no staging copy.
+  u32x4 v[kReorderMaxRows][kReorderPieces];
+#pragma unroll
+  for (int r = 0; r < kReorderMaxRows; ++r) {
+    if (par[r] == r) continue;
+#pragma unroll
+    for (int i = 0; i < kReorderPieces; ++i) {
+      const int64_t e = e0 + i * 256;
+      if (e < pieces) v[r][i] = base[par[r] * row_pieces + e];
+    }
   }
 #pragma unroll
-  for (int r = 0; r < kReorderMaxRows; ++r)
-    if (par[r] != r) base[r * row_pieces] = v[r];
+  for (int r = 0; r < kReorderMaxRows; ++r) {
+    if (par[r] == r) continue;
+#pragma unroll
+    for (int i = 0; i < kReorderPieces; ++i) {
+      const int64_t e = e0 + i * 256;
+      if (e < pieces) base[r * row_pieces + e] = v[r][i];
+    }
+  }
 }
 
 template <int G>
@@ -489,7 +505,8 @@ hipError_t launch_decode_attention(const AttnArgs& a, int rows, int group, hipSt
 
 hipError_t launch_cache_reorder(const ReorderArgs& a, int64_t planes, hipStream_t stream) {
   const int64_t pieces = a.length * (kD / 8);
-  const dim3 grid((unsigned)((pieces + 255) / 256), (unsigned)(planes * a.heads));
+  const int64_t per_block = 256 * kReorderPieces;
+  const dim3 grid((unsigned)((pieces + per_block - 1) / per_block), (unsigned)(planes * a.heads));
   hipLaunchKernelGGL(cache_reorder_kernel, grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }

@@ -355,6 +355,23 @@ def warp(scores, temperature, top_p, keep):
     return scores
 
 
+def multinomial_draws(probs, n):
+    """`torch.multinomial(probs, n)` without replacement as PyTorch computes
+    it -- the exponential race: the n largest of probs / q with q ~ Exp(1)
+    drawn from the default generator (argmax for n = 1) -- so the draws are
+    the same, without its input checks (the max, min and sum of probs, read
+    back to the host twice). `probs` here is a softmax output, finite and
+    non-negative by construction; n < 1 goes to torch.multinomial, which
+    rejects it as the reference's call would."""
+    if n < 1:
+        return torch.multinomial(probs, n)
+    q = torch.empty_like(probs).exponential_()
+    q = probs / q
+    if n == 1:
+        return torch.argmax(q, -1, keepdim=True)
+    return torch.topk(q, n).indices
+
+
 # Candidates kept per row by `warp_candidates`: the top-k plus room for values
 # tied with the k-th largest.
 TIE_ROOM = 14
@@ -438,7 +455,7 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
             scores = (log_probs + running_t[:, None]).view(1, -1)
             probs = scores.softmax(-1)
             possible = int(torch.count_nonzero(probs))
-        picks = torch.multinomial(probs, min(keep, possible))[0]
+        picks = multinomial_draws(probs, min(keep, possible))[0]
         picked = scores[0].gather(0, picks)
         # sorted(range(n), key=picked, reverse=True)[:beams]: descending, stable.
         ordered, order = torch.sort(picked, descending=True, stable=True)
