@@ -355,6 +355,13 @@ def warp(scores, temperature, top_p, keep):
     return scores
 
 
+def stable_descending(values):
+    """(sorted values, order) of a 1-D tensor, descending and stable --
+    `sorted(range(n), key=values.__getitem__, reverse=True)` in the
+    reference's survivor selection."""
+    return torch.sort(values, descending=True, stable=True)
+
+
 def multinomial_draws(probs, n):
     """`torch.multinomial(probs, n)` without replacement as PyTorch computes
     it -- the exponential race: the n largest of probs / q with q ~ Exp(1)
@@ -377,7 +384,7 @@ def multinomial_draws(probs, n):
 TIE_ROOM = 14
 
 
-def warp_candidates(scores, temperature, top_p, keep):
+def warp_candidates(scores, temperature, top_p, keep, with_index=False):
     """`warp` computed on each row's top-k candidates instead of the whole
     vocabulary: the same temperature, top-k threshold and top-p removal
     (runtime_shared.py:176-187), where the reference's full-vocabulary sort,
@@ -390,11 +397,14 @@ def warp_candidates(scores, temperature, top_p, keep):
 
     Returns (warped scores, overflow): overflow is a 0-d bool tensor that is
     True when a row may hold more values tied with the k-th largest than the
-    candidate set has room for; the caller then uses `warp`."""
+    candidate set has room for; the caller then uses `warp`. With
+    `with_index`, also the candidates' indices [rows, candidates]: every
+    entry outside them is -inf."""
     k = max(TOP_K, keep)
     vocab = scores.shape[-1]
     if k > vocab:  # the reference's top-k rejects it: same error
-        return warp(scores, temperature, top_p, keep), torch.zeros((), dtype=torch.bool)
+        out = warp(scores, temperature, top_p, keep), torch.zeros((), dtype=torch.bool)
+        return out + (None,) if with_index else out
     if temperature != 1.0:
         scores = scores / temperature
     kc = min(k + TIE_ROOM, vocab)
@@ -411,7 +421,7 @@ def warp_candidates(scores, temperature, top_p, keep):
         remove[..., -keep:] = False
         values = values.masked_fill(remove.flip(-1), float("-inf"))
     out = torch.full_like(scores, float("-inf")).scatter_(-1, index, values)
-    return out, overflow
+    return (out, overflow, index) if with_index else (out, overflow)
 
 
 def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, capacity=None,
@@ -445,11 +455,14 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
     history = []
     for step in range(steps):
         penalized = penalize(torch.log_softmax(logits.float(), -1), seen)
-        log_probs, overflow = warp_candidates(penalized, temperature, top_p, 2)
+        log_probs, overflow, candidates = warp_candidates(penalized, temperature, top_p, 2,
+                                                          with_index=True)
         scores = (log_probs + running_t[:, None]).view(1, -1)
         probs = scores.softmax(-1)
-        # One host read for the sample count and the tie check.
-        possible, overflow = torch.stack((torch.count_nonzero(probs), overflow.long())).tolist()
+        # One host read for the sample count and the tie check. Only the
+        # candidates can have a non-zero probability: count those.
+        possible = torch.count_nonzero(probs.view(beams, vocab).gather(1, candidates))
+        possible, overflow = torch.stack((possible, overflow.long())).tolist()
         if overflow:
             log_probs = warp(penalized, temperature, top_p, 2)
             scores = (log_probs + running_t[:, None]).view(1, -1)
@@ -458,7 +471,7 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
         picks = multinomial_draws(probs, min(keep, possible))[0]
         picked = scores[0].gather(0, picks)
         # sorted(range(n), key=picked, reverse=True)[:beams]: descending, stable.
-        ordered, order = torch.sort(picked, descending=True, stable=True)
+        ordered, order = stable_descending(picked)
         kept = min(beams, picks.numel())
         chosen = picks[order[:kept]]
         running_t = ordered[:kept]

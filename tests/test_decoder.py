@@ -250,3 +250,14 @@ def test_beam_steps_matches_host_selection_gpu(cuda_device):
         torch.manual_seed(5)
         got = beam_steps(model, emb, 8, beams=2)
     assert got[0] == want[0] and got[1] == want[1], (got, want)
+
+
+@pytest.mark.parametrize("values", ([3.0, 1.0, 3.0, 2.0], [1.0, 1.0, 1.0, 1.0], [0.5],
+                                    [-1e9, 2.0, 2.0, -1e9], [5.0, 4.0, 3.0, 2.0, 4.0, 5.0]))
+def test_stable_descending_is_python_sorted(values):
+    """The survivors' order: Python's sorted(..., reverse=True), ties in index
+    order (the reference's selection, runtime_shared.py:245)."""
+    got_values, got_order = decoder.stable_descending(torch.tensor(values))
+    want = sorted(range(len(values)), key=values.__getitem__, reverse=True)
+    assert got_order.tolist() == want
+    assert got_values.tolist() == [values[i] for i in want]
