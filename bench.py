@@ -106,7 +106,13 @@ def copies_for(nbytes, cap_bytes):
 
 
 def make_call(x, q, s, y, qtype, bias):
-    return lambda: native.gemv(x, q, s.view(torch.uint8), y, qtype, bias)
+    """One GEMV launch as quantization.soa_gemv makes it: with the per-stream
+    workspace that lets long rows split K (allocated at the warm-up call,
+    before any capture)."""
+    m, k = x.shape
+    n = y.shape[1]
+    return lambda: native.gemv(x, q, s.view(torch.uint8), y, qtype, bias,
+                               native.split_workspace(x.device, m, n, k, qtype))
 
 
 def capture(fns, stream):

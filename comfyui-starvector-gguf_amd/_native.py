@@ -66,6 +66,11 @@ def load() -> ctypes.CDLL:
         lib.svq_decode_attention.argtypes = [vp, i64, vp, vp, vp, vp, i64, vp, vp, i32, vp,
                                              i32, i32, i32, i32, ctypes.c_float, vp, i64, vp]
         lib.svq_decode_attention.restype = i32
+        lib.svq_gemv_split.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp,
+                                       i64, vp]
+        lib.svq_gemv_split.restype = i32
+        lib.svq_gemv_split_workspace.argtypes = [i32, i32, i32, i32]
+        lib.svq_gemv_split_workspace.restype = i64
         lib.svq_cache_reorder.argtypes = [vp, i64, i32, i32, i64, i32, i64, vp, vp]
         lib.svq_cache_reorder.restype = i32
         cp = ctypes.c_char_p
@@ -131,17 +136,66 @@ class _on_device:
 
 
 def gemv(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, y: torch.Tensor,
-         qtype: str, bias: torch.Tensor | None = None) -> None:
-    """y[m, n] = x[m, k] @ W[n, k]^T (+ bias); all tensors contiguous on one GPU."""
+         qtype: str, bias: torch.Tensor | None = None,
+         workspace: torch.Tensor | None = None) -> None:
+    """y[m, n] = x[m, k] @ W[n, k]^T (+ bias); all tensors contiguous on one GPU.
+    With a workspace (see split_workspace) and fp16 y, long rows split K
+    across workgroups (svq_gemv_split)."""
     lib = load()
     m, k = x.shape
     n = y.shape[1]
+    if workspace is not None and y.dtype == torch.float16:
+        _split(lib, x, q, s, y, qtype, bias, None, None, workspace)
+        return
     with _on_device(x.device):
         rc = lib.svq_gemv(x.data_ptr(), q.data_ptr(), s.data_ptr(),
                           None if bias is None else bias.data_ptr(), y.data_ptr(),
                           m, n, k, QTYPE_CODE[qtype], DTYPE_CODE[y.dtype],
                           _stream(x.device))
     _check(lib, "svq_gemv", rc)
+
+
+def _split(lib, x, q, s, y, qtype, bias, residual, activation, workspace) -> None:
+    if workspace.device != x.device or workspace.dtype != torch.uint8:
+        raise ValueError("workspace must be a uint8 tensor on the device of x")
+    m, k = x.shape
+    n = y.shape[1]
+    ptr = lambda t: None if t is None else t.data_ptr()
+    with _on_device(x.device):
+        rc = lib.svq_gemv_split(x.data_ptr(), q.data_ptr(), s.data_ptr(), ptr(bias),
+                                y.data_ptr(), m, n, k, QTYPE_CODE[qtype], ptr(residual),
+                                ACTIVATION_CODE[activation], workspace.data_ptr(),
+                                workspace.numel(), _stream(x.device))
+    _check(lib, "svq_gemv_split", rc)
+
+
+_split_workspaces: dict = {}
+
+
+def split_workspace(device: torch.device, m: int, n: int, k: int, qtype: str,
+                    allocate: bool = True, per_stream: bool = True) -> torch.Tensor | None:
+    """A workspace for svq_gemv_split of this shape, cached per (device,
+    stream) -- per device with per_stream False, for callers that keep all
+    their launches on one stream -- and grown as needed; None when the shape
+    runs in one pass, or when the workspace would have to grow while the
+    stream is being captured into a graph or `allocate` is False. Calls that
+    share it are ordered by their stream."""
+    if device.type != "cuda":
+        return None
+    lib = load()
+    need = lib.svq_gemv_split_workspace(m, n, k, QTYPE_CODE[qtype])
+    _check(lib, "svq_gemv_split_workspace", min(need, 0))
+    if need == 0:
+        return None
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, torch.cuda.current_stream(index).cuda_stream if per_stream else None)
+    ws = _split_workspaces.get(key)
+    if ws is None or ws.numel() < need:
+        if not allocate or torch.cuda.is_current_stream_capturing():
+            return None
+        ws = torch.empty(need, dtype=torch.uint8, device=torch.device("cuda", index))
+        _split_workspaces[key] = ws
+    return ws
 
 
 ACTIVATION_CODE = {None: 0, "gelu_tanh": 1}
@@ -151,9 +205,11 @@ def gemv_fused(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, y: torch.Tenso
                qtype: str, bias: torch.Tensor | None = None,
                ln_weight: torch.Tensor | None = None, ln_bias: torch.Tensor | None = None,
                ln_eps: float = 1e-5, residual: torch.Tensor | None = None,
-               activation: str | None = None) -> None:
+               activation: str | None = None, workspace: torch.Tensor | None = None) -> None:
     """y = residual + act(x' @ W^T + bias), x' = LayerNorm(x) when ln_weight or
-    ln_bias is given (svq_gemv_fused); fp16 tensors, contiguous, on one GPU."""
+    ln_bias is given (svq_gemv_fused); fp16 tensors, contiguous, on one GPU.
+    Without a LayerNorm and with a workspace, long rows split K across
+    workgroups (svq_gemv_split)."""
     lib = load()
     m, k = x.shape
     n = y.shape[1]
@@ -167,6 +223,9 @@ def gemv_fused(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, y: torch.Tenso
         raise ValueError(f"residual must be a contiguous float16 {tuple(y.shape)} tensor")
     if y.dtype != torch.float16:
         raise ValueError("svq_gemv_fused writes float16")
+    if workspace is not None and ln_weight is None and ln_bias is None:
+        _split(lib, x, q, s, y, qtype, bias, residual, activation, workspace)
+        return
     ptr = lambda t: None if t is None else t.data_ptr()
     with _on_device(x.device):
         rc = lib.svq_gemv_fused(x.data_ptr(), q.data_ptr(), s.data_ptr(), ptr(bias),

@@ -94,7 +94,15 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 
   const int n = a.n, k = a.k;
   const int kb = k >> 5;
-  const int units = kb * T::kUnitsPerBlock;
+  // K slices across workgroups (a.partial set, a.slices >= 2): workgroup b
+  // takes slice b % SL of every row -- units ubase .. ubase + units, x
+  // staged for that slice only -- and writes raw partial sums. Otherwise one
+  // slice: the whole row.
+  const int SL = a.partial ? a.slices : 1;
+  const int slice = (int)blockIdx.x % SL;
+  const int units = kb * T::kUnitsPerBlock / SL;
+  const int ubase = slice * units;
+  const int bx = (int)blockIdx.x / SL;  // workgroup within its slice
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slot = lane >> 2;  // MFMA block: the unit slot of this lane
@@ -109,7 +117,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   const int tile_rows = 4 * R;
   const int tiles = (n + tile_rows - 1) / tile_rows;
   const int groups = (tiles + P - 1) / P;
-  const int G = gridDim.x;
+  const int G = (int)gridDim.x / SL;
   // At most one tile per wave (S = 1): wave-major tiles (wave p of
   // workgroup g owns tile wv = p * G + g), which spreads the idle waves of a
   // short matrix over all workgroups, hence over all CUs. Otherwise workgroup
@@ -119,18 +127,17 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   // walks the same number of tile groups.
   const int WV = P * G;
   const bool wave_major = S == 1 && tiles <= WV;
-  const int wv = p_id * G + (int)blockIdx.x;
-  const int my_tiles = wave_major
-                           ? (wv < tiles ? 1 : 0)
-                           : ((int)blockIdx.x < groups ? (groups - (int)blockIdx.x + G - 1) / G : 0);
+  const int wv = p_id * G + bx;
+  const int my_tiles = wave_major ? (wv < tiles ? 1 : 0)
+                                  : (bx < groups ? (groups - bx + G - 1) / G : 0);
   const int niter_all = (units + kSlots * U - 1) / (kSlots * U);
   const int st0 = sk * niter_all / S, st1 = (sk + 1) * niter_all / S;
   const int steps = my_tiles * (st1 - st0);
-  auto tile_of = [&](int j) { return wave_major ? wv + j * WV : ((int)blockIdx.x + j * G) * P + p_id; };
+  auto tile_of = [&](int j) { return wave_major ? wv + j * WV : (bx + j * G) * P + p_id; };
   // A workgroup without tiles leaves before staging x (the same decision for
   // all its waves): wave-major, when its first wave (wv = g) has none;
   // otherwise when it has no tile group.
-  if ((int)blockIdx.x >= (wave_major ? tiles : groups)) return;
+  if (bx >= (wave_major ? tiles : groups)) return;
   const uint32_t row_bytes = (uint32_t)kb * T::kBlockQ;
 
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)n * row_bytes);
@@ -169,12 +176,13 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
     const int u = U * (slot + pit * kSlots);
     const bool valid = pj < my_tiles && u < units;
     const uint32_t oob = (uint32_t)(!valid) * kOutOfRange;
+    const uint32_t ug = (uint32_t)(ubase + u);  // unit within the whole row
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if constexpr (U == 3 && QT == 5) {
         // Three 20-byte blocks: 60 contiguous bytes as 3 x 16 + 12.
         typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-        const uint32_t off = pqo[r] + (uint32_t)u * 20u + oob;
+        const uint32_t off = pqo[r] + ug * 20u + oob;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
           const u32x4 v = __builtin_bit_cast(
@@ -187,7 +195,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
         w[d][r][12] = t.x; w[d][r][13] = t.y; w[d][r][14] = t.z;
       } else if constexpr (U > 1) {
         // U consecutive 16-byte units: U x 16 contiguous bytes.
-        const uint32_t off = pqo[r] + (uint32_t)u * 16u + oob;
+        const uint32_t off = pqo[r] + ug * 16u + oob;
 #pragma unroll
         for (int c = 0; c < U; ++c) {
           const u32x4 v = __builtin_bit_cast(
@@ -198,17 +206,17 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
       }
       if constexpr (U == 3) {
         // Three consecutive blocks (one unit each): their three scales.
-        const uint32_t soff = pso[r] + (uint32_t)u * 2u + oob;
+        const uint32_t soff = pso[r] + ug * 2u + oob;
         sc[d][r][0] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff, 0, 0);
         sc[d][r][1] = __builtin_amdgcn_raw_buffer_load_b32(sr, soff + 2u, 0, 0);
       } else if constexpr (U == 2) {
         // The two halves of one Q8_0 block (u even): one scale.
         sc[d][r][0] = __builtin_amdgcn_raw_buffer_load_b16(
-            sr, pso[r] + (uint32_t)(u / 2) * 2u + oob, 0, 0);
+            sr, pso[r] + (ug / 2u) * 2u + oob, 0, 0);
       } else {
-        load_unit_buf<QT>(qr, pqo[r] + (uint32_t)u * T::kUnitBytes + oob, w[d][r]);
+        load_unit_buf<QT>(qr, pqo[r] + ug * T::kUnitBytes + oob, w[d][r]);
         sc[d][r][0] = __builtin_amdgcn_raw_buffer_load_b16(
-            sr, pso[r] + (uint32_t)(u / T::kUnitsPerBlock) * 2u + oob, 0, 0);
+            sr, pso[r] + (ug / T::kUnitsPerBlock) * 2u + oob, 0, 0);
       }
     }
     if (++pit == st1) {
@@ -230,7 +238,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 
   // x loads first, then the weight prologue, then x is written to LDS
   // (vector loads retire in issue order).
-  XStager<QT, M, WPG * 64, kStage4Batch<QT, M>, Mfma4Traits<QT>::kSxMul, LN> st(a.x, k, 0, units,
+  XStager<QT, M, WPG * 64, kStage4Batch<QT, M>, Mfma4Traits<QT>::kSxMul, LN> st(a.x, k, ubase, units,
                                                                                units);
   st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
   st.begin(lns);
@@ -328,11 +336,17 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
           for (int r = 0; r < R; ++r) {
             const int row = tile * tile_rows + r * 4 + ri;
             if (row < n) {
-              const float b = half_bits_to_float((uint16_t)bias_bits[r]);
+              if (SL > 1) {  // raw slice sums; split_finish scales, biases and stores
 #pragma unroll
-              for (int m = 0; m < M; ++m) {
-                const float v = __builtin_fmaf(acc[r][m], Mfma4Traits<QT>::kOutScale, b);
-                store_y(a, m, row, v);
+                for (int m = 0; m < M; ++m)
+                  a.partial[((size_t)slice * M + m) * n + row] = acc[r][m];
+              } else {
+                const float b = half_bits_to_float((uint16_t)bias_bits[r]);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                  const float v = __builtin_fmaf(acc[r][m], Mfma4Traits<QT>::kOutScale, b);
+                  store_y(a, m, row, v);
+                }
               }
             }
           }
@@ -347,6 +361,20 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
       }
     }
   }
+}
+
+// Second kernel of the K split: y[m, row] = store(sum over the slices, in
+// slice order, of the raw partial sums, times the code scaling, plus bias),
+// with the same epilogue (rounding, GELU, residual) as the one-pass store.
+__global__ __launch_bounds__(256) void split_finish_kernel(GemvArgs a, int m_rows,
+                                                           float out_scale) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= m_rows * a.n) return;
+  const int m = i / a.n, row = i - m * a.n;
+  float v = 0.f;
+  for (int sl = 0; sl < a.slices; ++sl) v += a.partial[((size_t)sl * m_rows + m) * a.n + row];
+  const float b = a.bias ? half_bits_to_float(a.bias[row]) : 0.f;
+  store_y(a, m, row, __builtin_fmaf(v, out_scale, b));
 }
 
 template <int QT, int M, int R, int D, int U, bool LN>
@@ -427,6 +455,17 @@ size_t mfma4_lds_bytes(int qtype, int m, int k, int rows, int ksplit) {
 
 hipError_t launch_gemv_mfma4(const GemvArgs& a, int qtype, int m, int rows, int groups,
                              hipStream_t stream) {
+  if (a.partial) {  // K slices: x staged per slice, then the slices added
+    const hipError_t e = mfma4_dispatch(a, false, qtype, m, rows, groups,
+                                        mfma4_lds_bytes(qtype, m, a.k / a.slices, rows, 1),
+                                        stream, nullptr);
+    if (e != hipSuccess) return e;
+    const float out_scale = qtype == 8 ? Mfma4Traits<8>::kOutScale : Mfma4Traits<4>::kOutScale;
+    const int total = m * a.n;
+    hipLaunchKernelGGL(split_finish_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, a,
+                       m, out_scale);
+    return hipGetLastError();
+  }
   return mfma4_dispatch(a, a.ln_w || a.ln_b, qtype, m, rows, groups,
                         mfma4_lds_bytes(qtype, m, a.k, rows, a.ksplit) +
                             layer_norm_lds_bytes(a.k, a.ln_w || a.ln_b),

@@ -25,6 +25,11 @@ struct GemvArgs {
   float ln_eps;              //   (no LayerNorm when both are nullptr)
   const uint16_t* residual;  // fp16 [m, n] added to the rounded output, or nullptr
   int act;                   // 0 none, 1 tanh-approximated GELU of the rounded output
+  // K split across workgroups (streaming MFMA kernel): with `partial` set,
+  // workgroup b takes K slice b % slices of every row and writes its raw sums
+  // to partial[slice][m][n]; split_finish adds the slices and stores y.
+  int slices;
+  float* partial;
 };
 
 struct GemvShape {

@@ -124,7 +124,10 @@ class Starcoder2Block(nn.Module):
                                     bias, out, heads, kvh, hd ** -0.5, workspace)
             x = fused_linear(self.o_proj, out, residual=x)
             h = fused_linear(self.c_fc, x, norm=self.post_attention_layernorm, gelu=True)
-            return fused_linear(self.c_proj, h, residual=x).view(rows, 1, hidden)
+            split = native.split_workspace(x.device, rows, hidden, cfg.inner,
+                                           self.c_proj._specs["weight"].qtype,
+                                           allocate=False, per_stream=False)
+            return fused_linear(self.c_proj, h, residual=x, workspace=split).view(rows, 1, hidden)
         qkv = self.qkv_proj(self.input_layernorm(x))
         out = self.torch_attention(qkv, cos, sin, keys, values, position, bias)
         x = x + self.o_proj(out)
@@ -156,10 +159,11 @@ class Starcoder2Block(nn.Module):
         return torch.bmm(probs, values.flatten(0, 1)).view(rows, 1, hidden)
 
 
-def fused_linear(linear, x, norm=None, residual=None, gelu=False):
+def fused_linear(linear, x, norm=None, residual=None, gelu=False, workspace=None):
     """`linear` (a GGUFLinear) on fp16 rows x [m, k] with the ops around it in
     one `svq_gemv_fused` launch: residual + gelu(linear(norm(x))), each part
-    optional, rounded to fp16 after every op as the separate torch ops are."""
+    optional, rounded to fp16 after every op as the separate torch ops are.
+    With a workspace and no norm, long rows split K (`svq_gemv_split`)."""
     spec = linear._specs["weight"]
     n, k = spec.shape
     if x.shape[-1] != k or x.dim() != 2:
@@ -170,7 +174,7 @@ def fused_linear(linear, x, norm=None, residual=None, gelu=False):
                       ln_weight=None if norm is None else norm.weight,
                       ln_bias=None if norm is None else norm.bias,
                       ln_eps=1e-5 if norm is None else norm.eps, residual=residual,
-                      activation="gelu_tanh" if gelu else None)
+                      activation="gelu_tanh" if gelu else None, workspace=workspace)
     return y
 
 
@@ -274,6 +278,9 @@ class CachedDecoding:
             cfg = model.cfg
             native.attention_workspace(keys.device, keys.shape[1], cfg.heads, cfg.kv_heads,
                                        keys.shape[3])
+            native.split_workspace(keys.device, keys.shape[1], cfg.hidden, cfg.inner,
+                                   model.layers[0].c_proj._specs["weight"].qtype,
+                                   per_stream=False)
 
     def span(self):
         return min(self.keys.shape[-2], max(512, 1 << self.length.bit_length()))

@@ -224,7 +224,10 @@ def soa_gemv(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor,
     total = n * (k // 32)
     if q.numel() != total * (BLOCK_BYTES[qtype] - 2) or s.numel() != total:
         raise ValueError("Incorrect repacked weight size")
-    _native.gemv(_aligned(x, 16), _aligned(q, 16), s, out, qtype, bias)
+    # Long rows split K across workgroups through a per-stream workspace
+    # (svq_gemv_split); during graph capture without one, a single pass.
+    workspace = _native.split_workspace(x.device, x.shape[0], n, k, qtype)
+    _native.gemv(_aligned(x, 16), _aligned(q, 16), s, out, qtype, bias, workspace)
 
 
 # Static activation/output pairs of decode graphs (reference

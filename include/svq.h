@@ -115,6 +115,29 @@ int svq_gemv_fused(const void *x, const uint8_t *q, const uint16_t *s,
                    const uint16_t *residual, int activation, void *stream);
 
 /*
+ * svq_gemv_fused without the LayerNorm, with a caller-provided workspace
+ * that lets long rows (K > 8192 at m = 2..4) split K across workgroups: each
+ * workgroup stages only a slice of x (at most 4608 columns) and writes fp32
+ * partial sums to the workspace, and a second kernel adds the slices in a
+ * fixed order and applies bias, activation and residual. Same results as
+ * svq_gemv_fused within fp32 summation order; shapes that do not split, or a
+ * workspace smaller than svq_gemv_split_workspace reports, run in one pass.
+ * Replaces the same reference calls as svq_gemv / svq_gemv_fused
+ * (quantization.py:232-265; runtime_8b.py:57 for c_proj with its residual).
+ *   workspace  device memory, 16-byte aligned, or NULL; calls sharing one
+ *              must not overlap (same stream, or ordered by events)
+ * y is fp16.
+ */
+int svq_gemv_split(const void *x, const uint8_t *q, const uint16_t *s,
+                   const uint16_t *bias, void *y, int m, int n, int k, int qtype,
+                   const uint16_t *residual, int activation, void *workspace,
+                   int64_t workspace_bytes, void *stream);
+
+/* Bytes of workspace svq_gemv_split uses for this shape (0: one pass), or a
+   negative SVQ_E* code for an invalid shape. */
+int64_t svq_gemv_split_workspace(int m, int n, int k, int qtype);
+
+/*
  * Diagnostic with no counterpart in the reference (whose launch tuple is the
  * per-(qtype, M) table SOA_GEMV_CONFIG, quantization.py:121-127): the launch
  * svq_gemv would make for this shape on the current device, as

@@ -197,3 +197,37 @@ def gemv_fused(**kw):
 def test_gemv_fused_rejects_bad_arguments(kw, code):
     assert gemv_fused(**kw) == code
     assert native.load().svq_last_error().decode()
+
+
+def gemv_split(**kw):
+    args = dict(x=FAKE, q=FAKE, s=FAKE, bias=None, y=FAKE + 1024, m=2, n=8, k=64, qtype=4,
+                res=None, act=0, ws=FAKE, ws_bytes=1 << 20)
+    args.update(kw)
+    return native.load().svq_gemv_split(
+        args["x"], args["q"], args["s"], args["bias"], args["y"], args["m"], args["n"],
+        args["k"], args["qtype"], args["res"], args["act"], args["ws"], args["ws_bytes"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(act=2), -4), (dict(res=FAKE + 1), -6), (dict(ws=FAKE + 8), -6),
+    (dict(y=FAKE, res=FAKE + 64), -2), (dict(ws_bytes=-1), -7),
+    (dict(qtype=3), -1), (dict(m=9), -2), (dict(k=40), -2), (dict(x=None), -3),
+])
+def test_gemv_split_rejects_bad_arguments(kw, code):
+    assert gemv_split(**kw) == code
+    assert native.load().svq_last_error().decode()
+
+
+def test_gemv_split_workspace_size():
+    """fp32 partial sums of every slice: K > 8192 at m = 2..4 is cut into the
+    fewest slices of at most 4608 columns that divide K / 32."""
+    lib = native.load()
+    assert lib.svq_gemv_split_workspace(2, 4608, 18432, 5) == 4 * 2 * 4608 * 4
+    assert lib.svq_gemv_split_workspace(1, 4608, 18432, 4) == 0   # m = 1: one pass
+    assert lib.svq_gemv_split_workspace(4, 100, 9216, 8) == 2 * 4 * 100 * 4
+    assert lib.svq_gemv_split_workspace(2, 100, 12288, 4) == 3 * 2 * 100 * 4
+    assert lib.svq_gemv_split_workspace(2, 4608, 4608, 5) == 0   # one pass
+    assert lib.svq_gemv_split_workspace(2, 2048, 8192, 4) == 0   # K <= 8192
+    assert lib.svq_gemv_split_workspace(5, 4608, 18432, 5) == 0  # m > 4
+    assert lib.svq_gemv_split_workspace(2, 64, 40, 4) == -2
+    assert lib.svq_gemv_split_workspace(2, 64, 64, 3) == -1

@@ -163,3 +163,72 @@ def test_decoder_layer_sequence(cuda_device):
     proj_ref = dict(proj, x=want_h)
     want = torch_ref(proj_ref, res=True).float()
     assert (got - want).abs().max().item() <= 3e-3 * want.abs().max().item()
+
+
+SPLIT_SHAPES = [
+    (2, 4608, 18432, "Q5_0"),  # 8B c_proj at beam 2: four slices of 4608
+    (2, 4608, 18432, "Q4_0"),
+    (2, 4608, 18432, "Q8_0"),
+    (4, 130, 18432, "Q4_0"),   # ragged rows
+    (3, 77, 9216, "Q8_0"),     # two slices
+    (2, 300, 12288, "Q5_0"),   # three slices
+    (4, 64, 18432, "Q5_0"),
+]
+
+
+def split(c, qtype, ws, res=False, gelu=False):
+    y = torch.empty((c["x"].shape[0], c["w"].shape[0]), dtype=torch.float16, device=c["x"].device)
+    native.gemv_fused(c["x"], c["q"], c["s"], y, qtype, bias=c["bias"],
+                      residual=c["res"] if res else None,
+                      activation="gelu_tanh" if gelu else None, workspace=ws)
+    return y
+
+
+@pytest.mark.parametrize("m,n,k,qtype", SPLIT_SHAPES)
+def test_split_k_matches_torch_and_one_pass(cuda_device, m, n, k, qtype):
+    """svq_gemv_split (K slices across workgroups, then the finish kernel)
+    against the fp32 torch reference and the one-pass kernels, with every
+    epilogue; the slices only reorder fp32 sums."""
+    c = make(m, n, k, qtype, cuda_device, seed=8)
+    ws = native.split_workspace(cuda_device, m, n, k, qtype)
+    # cached per stream and only grown: at least this shape's size
+    assert ws is not None and ws.numel() >= native.load().svq_gemv_split_workspace(
+        m, n, k, native.QTYPE_CODE[qtype])
+    for kw in (dict(), dict(res=True), dict(gelu=True), dict(res=True, gelu=True)):
+        got = split(c, qtype, ws, **kw).float()
+        want = torch_ref(c, **kw).float()
+        assert (got - want).abs().max().item() <= 3e-3 * want.abs().max().item(), kw
+        one = fused(c, qtype, **kw).float()
+        assert (got - one).abs().max().item() <= 1e-3 * one.abs().max().item(), kw
+    # svq_gemv with a workspace takes the same path
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda_device)
+    native.gemv(c["x"], c["q"], c["s"], y, qtype, c["bias"], ws)
+    assert torch.equal(y, split(c, qtype, ws))
+
+
+def test_split_k_residual_in_place_and_graph_replays(cuda_device):
+    """In-place residual (y is the residual) and graph replays of the split
+    launches on the stream that allocated the workspace: every replay equals
+    the eager result."""
+    m, n, k, qtype = 2, 4608, 18432, "Q4_0"
+    c = make(m, n, k, qtype, cuda_device, seed=9)
+    stream = torch.cuda.Stream(cuda_device)
+    with torch.cuda.stream(stream):
+        ws = native.split_workspace(cuda_device, m, n, k, qtype)
+        y = c["res"].clone()
+        native.gemv_fused(c["x"], c["q"], c["s"], y, qtype, bias=c["bias"], residual=y,
+                          workspace=ws)
+        stream.synchronize()
+        eager = y.clone()
+        assert torch.equal(eager, (c["res"] + split(c, qtype, ws)))
+        out = torch.empty((m, n), dtype=torch.float16, device=cuda_device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out.copy_(c["res"])
+            native.gemv_fused(c["x"], c["q"], c["s"], out, qtype, bias=c["bias"], residual=out,
+                              workspace=native.split_workspace(cuda_device, m, n, k, qtype))
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
