@@ -204,6 +204,23 @@ def _is_gemv(name):
     return name.startswith("void svq::") and "gemv" in name
 
 
+def _is_split_finish(name):
+    """Second kernel of a K split across workgroups (part of the GEMV before it)."""
+    return "split_finish_kernel" in name
+
+
+def _fold_split_finish(rows, key="Kernel_Name"):
+    """GEMV dispatches in launch order, each K-split GEMV with its finish
+    kernel attached under "_finish"."""
+    out = []
+    for r in rows:
+        if _is_split_finish(r[key]) and out:
+            out[-1] = dict(out[-1], _finish=r)
+        elif _is_gemv(r[key]):
+            out.append(r)
+    return out
+
+
 def _short_kernel(name):
     for junk in ("void svq::", "(anonymous namespace)::", "(svq::GemvArgs)"):
         name = name.replace(junk, "")
@@ -217,7 +234,10 @@ def _read_csv(path):
 
 
 def _durations_us(rows):
-    return [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows]
+    """Kernel durations; a K-split GEMV counts both of its kernels."""
+    def one(r):
+        return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    return [one(r) + (one(r["_finish"]) if "_finish" in r else 0.0) for r in rows]
 
 
 def _counter_dispatches(path):
@@ -249,7 +269,7 @@ def summarize(root: Path):
     for trace in sorted(root.rglob("*kernel_trace.csv")):
         # Rows are written as dispatches complete; launch order is Dispatch_Id.
         rows = sorted(_read_csv(trace), key=lambda r: int(r["Dispatch_Id"]))
-        gemv = [r for r in rows if _is_gemv(r["Kernel_Name"])]
+        gemv = _fold_split_finish(rows)
         copies = [r for r in rows if "copyBuffer" in r["Kernel_Name"]]
         out.append(f"kernel trace: {trace.relative_to(root)} ({len(gemv)} GEMV dispatches)")
         if len(gemv) == profile_dispatches:
@@ -261,7 +281,10 @@ def summarize(root: Path):
                 durs = _durations_us(mine)
                 avg = sum(durs) / len(durs)
                 nbytes = algorithmic_bytes(STEP_QTYPE, n, k, STEP_M, bias)
-                out.append(f"| {name} {n}x{k} | {_short_kernel(mine[0]['Kernel_Name'])} | "
+                kname = _short_kernel(mine[0]["Kernel_Name"])
+                if "_finish" in mine[0]:
+                    kname += " + split_finish_kernel"
+                out.append(f"| {name} {n}x{k} | {kname} | "
                            f"{mine[0]['Grid_Size_X']} | {mine[0]['VGPR_Count']} | "
                            f"{mine[0]['LDS_Block_Size']} | {len(mine)} | {avg:.2f} | {min(durs):.2f} | "
                            f"{nbytes / avg / 1e3:.0f} | {nbytes / avg / 1e3 / PEAK_HBM_GBS:.1%} |")
@@ -287,7 +310,7 @@ def summarize(root: Path):
         out.append("| kernel | calls | avg us | min us | max us | % of GPU time |")
         out.append("|---|---|---|---|---|---|")
         for r in _read_csv(stats):
-            if _is_gemv(r["Name"]) or "copyBuffer" in r["Name"]:
+            if _is_gemv(r["Name"]) or _is_split_finish(r["Name"]) or "copyBuffer" in r["Name"]:
                 out.append(f"| {_short_kernel(r['Name'])} | {r['Calls']} | "
                            f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
                            f"{float(r['MaxNs']) / 1e3:.2f} | {r['Percentage']} |")
@@ -296,7 +319,13 @@ def summarize(root: Path):
     scale = {}       # counter -> bytes per unit the counter reports
     for coll in sorted(root.rglob("*counter_collection.csv")):
         disp = _counter_dispatches(coll)
-        gemv = [c for name, c in disp if _is_gemv(name)]
+        gemv = []
+        for name, c in disp:  # a K split's finish kernel adds to its GEMV
+            if _is_split_finish(name) and gemv:
+                gemv[-1] = {key: gemv[-1].get(key, 0.0) + c.get(key, 0.0)
+                            for key in set(gemv[-1]) | set(c)}
+            elif _is_gemv(name):
+                gemv.append(c)
         copies = [c for name, c in disp if "copyBuffer" in name]
         names = sorted({n for c in gemv + copies for n in c})
         out.append(f"counters: {coll.relative_to(root)}")
@@ -471,7 +500,8 @@ def summarize_decode(trace: Path):
     phase = rows[last + 1:]
     durs = _durations_us(phase)
     total = sum(durs)
-    gemv = sum(d for d, r in zip(durs, phase) if _is_gemv(r["Kernel_Name"]))
+    gemv = sum(d for d, r in zip(durs, phase)
+               if _is_gemv(r["Kernel_Name"]) or _is_split_finish(r["Kernel_Name"]))
     by = {}
     for d, r in zip(durs, phase):
         key = _short_kernel(r["Kernel_Name"])[:70]
