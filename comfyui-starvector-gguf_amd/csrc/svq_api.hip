@@ -371,7 +371,7 @@ struct Fusion {
 int split_slices(int m, int k, bool layer_norm) {
   if (layer_norm || m < 2 || m > 4 || k <= 8192) return 0;
   const int kb = k / 32;
-  for (int sl = 2; sl <= 8; ++sl)
+  for (int sl = 2; sl <= svq::kSplitMaxSlices; ++sl)
     if (kb % sl == 0 && k / sl <= 4608) return sl;
   return 0;
 }

@@ -658,6 +658,20 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // fp32 output as is; fp16 output rounded, then GELU (rounded again), then
 // the residual added (rounded again), each step as the separate fp16 torch op
 // it replaces.
+// store_y of element i with its residual already loaded (`res`, the fp16
+// bits; unused without a residual or with fp32 output).
+__device__ __forceinline__ void store_y_loaded(const GemvArgs& a, size_t i, float v,
+                                               uint16_t res) {
+  if (a.y_f32) {
+    reinterpret_cast<float*>(a.y)[i] = v;
+    return;
+  }
+  _Float16 t = (_Float16)v;
+  if (a.act == 1) t = (_Float16)gelu_tanh((float)t);
+  if (a.residual) t = (_Float16)(half_bits_to_float(res) + (float)t);
+  reinterpret_cast<_Float16*>(a.y)[i] = t;
+}
+
 __device__ __forceinline__ void store_y(const GemvArgs& a, int m, int row, float v) {
   const size_t i = (size_t)m * a.n + row;
   if (a.y_f32) {

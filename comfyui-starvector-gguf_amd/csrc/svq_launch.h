@@ -28,9 +28,10 @@ struct GemvArgs {
   // K split across workgroups (streaming MFMA kernel): with `partial` set,
   // workgroup b takes K slice b % slices of every row and writes its raw sums
   // to partial[slice][m][n]; split_finish adds the slices and stores y.
-  int slices;
+  int slices;  // 2..kSplitMaxSlices with `partial`
   float* partial;
 };
+constexpr int kSplitMaxSlices = 8;
 
 struct GemvShape {
   int m;
