@@ -73,6 +73,9 @@ def load() -> ctypes.CDLL:
         lib.svq_gemv_split_workspace.restype = i64
         lib.svq_cache_reorder.argtypes = [vp, i64, i32, i32, i64, i32, i64, vp, vp]
         lib.svq_cache_reorder.restype = i32
+        lib.svq_beam_select.argtypes = [vp, vp, vp, vp, i32, i64, i32, i32, vp, vp, i64, vp, vp,
+                                        vp, vp, vp]
+        lib.svq_beam_select.restype = i32
         cp = ctypes.c_char_p
         lib.svq_gguf_open.argtypes = [cp, i32, ctypes.POINTER(vp)]
         lib.svq_gguf_open.restype = i32
@@ -348,6 +351,44 @@ def cache_reorder(cache: torch.Tensor, parents: torch.Tensor, length: int) -> No
         rc = lib.svq_cache_reorder(cache.data_ptr(), planes, rows, heads, capacity, head_dim,
                                    int(length), parents.data_ptr(), _stream(cache.device))
     _check(lib, "svq_cache_reorder", rc)
+
+
+def beam_select(probs, noise, scores, candidates, draws, seen_in, seen_out, running, parents,
+                tokens, tokens_copy=None) -> None:
+    """Survivor selection of a beam-sampling step (svq_beam_select) on the
+    device, asynchronously: `draws` multinomial draws without replacement
+    from probs (the exponential race with the given Exp(1) noise, over the
+    candidate token ids [beams, ncand] only), the first `beams` of them by
+    score (descending, stable), their parents and tokens, running scores, and
+    seen rows seen_out[b] = seen_in[parent b] with token b set. probs, noise
+    and scores are float32 with beams * vocab entries; seen_in / seen_out are
+    distinct bool [beams, pitch] buffers, pitch >= vocab a multiple of 16."""
+    lib = load()
+    beams, ncand = candidates.shape
+    tensors = (probs, noise, scores, candidates, seen_in, seen_out, running, parents, tokens) + (
+        (tokens_copy,) if tokens_copy is not None else ())
+    if any(not t.is_contiguous() or t.device != probs.device for t in tensors):
+        raise ValueError("beam_select tensors must be contiguous and on one device")
+    if any(t.dtype != torch.float32 for t in (probs, noise, scores, running)):
+        raise ValueError("probs, noise, scores and running must be float32")
+    if any(t.dtype != torch.int64 for t in tensors[7:] + (candidates,)):
+        raise ValueError("candidates, parents and tokens must be int64")
+    if seen_in.dtype != torch.bool or seen_out.dtype != torch.bool or seen_in.dim() != 2:
+        raise ValueError("seen_in and seen_out must be bool [beams, pitch]")
+    if probs.numel() % beams or noise.numel() != probs.numel() or scores.numel() != probs.numel():
+        raise ValueError("probs, noise and scores must hold beams * vocab entries")
+    if seen_out.shape != seen_in.shape or seen_in.shape[0] != beams:
+        raise ValueError("seen_in and seen_out must be [beams, pitch]")
+    if any(t.numel() != beams for t in (running, parents, tokens)):
+        raise ValueError("running, parents and tokens must hold one entry per beam")
+    with _on_device(probs.device):
+        rc = lib.svq_beam_select(
+            probs.data_ptr(), noise.data_ptr(), scores.data_ptr(), candidates.data_ptr(), beams,
+            probs.numel() // beams, ncand, int(draws), seen_in.data_ptr(), seen_out.data_ptr(),
+            seen_in.shape[1], running.data_ptr(), parents.data_ptr(), tokens.data_ptr(),
+            tokens_copy.data_ptr() if tokens_copy is not None else None,
+            _stream(probs.device))
+    _check(lib, "svq_beam_select", rc)
 
 
 def pack_soa(aos_ptr: int, nblocks: int, qtype: str, q: torch.Tensor, s: torch.Tensor,

@@ -676,4 +676,37 @@ int svq_cache_reorder(uint16_t* cache, int64_t planes, int rows, int heads, int6
   return 0;
 }
 
+int svq_beam_select(const float* probs, const float* noise, const float* scores,
+                    const int64_t* candidates, int beams, int64_t vocab, int ncand, int draws,
+                    const uint8_t* seen_in, uint8_t* seen_out, int64_t seen_pitch,
+                    float* running, int64_t* parents, int64_t* tokens, int64_t* tokens_copy,
+                    void* stream) {
+  if (beams < 1 || beams > svq::kBeamMaxRows || vocab < 1 || ncand < 1 || ncand > vocab ||
+      (int64_t)beams * ncand > svq::kBeamMaxCandidates || draws < 1 || draws > 2 * beams ||
+      draws > beams * ncand || seen_pitch < vocab || seen_pitch % 16 != 0)
+    return fail(SVQ_E_SHAPE,
+                "invalid beam selection beams=%d vocab=%lld candidates=%d draws=%d "
+                "seen_pitch=%lld",
+                beams, (long long)vocab, ncand, draws, (long long)seen_pitch);
+  if ((int64_t)beams * vocab >= ((int64_t)1 << 40) || (int64_t)beams * seen_pitch >= ((int64_t)1 << 40))
+    return fail(SVQ_E_RANGE, "beam selection too large");
+  if (!probs || !noise || !scores || !candidates || !seen_in || !seen_out || !running ||
+      !parents || !tokens)
+    return fail(SVQ_E_NULL, "NULL beam selection argument");
+  if (!aligned(probs, 4) || !aligned(noise, 4) || !aligned(scores, 4) || !aligned(running, 4) ||
+      !aligned(candidates, 8) || !aligned(parents, 8) || !aligned(tokens, 8) ||
+      (tokens_copy && !aligned(tokens_copy, 8)) || !aligned(seen_in, 16) || !aligned(seen_out, 16))
+    return fail(SVQ_E_ALIGN, "misaligned beam selection argument");
+  const int64_t seen_bytes = (int64_t)beams * seen_pitch;
+  const uint8_t* out_lo = seen_out;
+  if (seen_in < out_lo + seen_bytes && out_lo < seen_in + seen_bytes)
+    return fail(SVQ_E_SHAPE, "seen_in and seen_out overlap");
+  svq::BeamSelectArgs a{probs,   noise,       scores, candidates, seen_in, seen_out,
+                        seen_pitch, running, parents, tokens,     tokens_copy, vocab,
+                        beams,   ncand,       draws};
+  const hipError_t e = svq::launch_beam_select(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "svq_beam_select launch");
+  return 0;
+}
+
 }  // extern "C"

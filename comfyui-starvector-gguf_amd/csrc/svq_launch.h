@@ -118,6 +118,28 @@ struct ReorderArgs {
 };
 hipError_t launch_cache_reorder(const ReorderArgs& a, int64_t planes, hipStream_t stream);
 
+// Survivor selection of a beam-sampling step (svq_beam_select).
+constexpr int kBeamMaxRows = 8;
+constexpr int kBeamMaxCandidates = 1024;  // beams x candidates per beam
+struct BeamSelectArgs {
+  const float* probs;         // [beams * vocab]
+  const float* noise;         // [beams * vocab] Exp(1) draws
+  const float* scores;        // [beams * vocab]
+  const int64_t* candidates;  // [beams, ncand] token ids
+  const uint8_t* seen_in;     // [beams, seen_pitch]
+  uint8_t* seen_out;          // [beams, seen_pitch]
+  int64_t seen_pitch;         // bytes per seen row, a multiple of 16
+  float* running;             // [beams] out
+  int64_t* parents;           // [beams] out
+  int64_t* tokens;            // [beams] out
+  int64_t* tokens_copy;       // [beams] out, or NULL
+  int64_t vocab;
+  int beams;
+  int ncand;
+  int draws;
+};
+hipError_t launch_beam_select(const BeamSelectArgs& a, hipStream_t stream);
+
 hipError_t launch_dequant(const uint8_t* q, const uint16_t* s, void* out,
                           int64_t nblocks, int qtype, int out_dtype,
                           hipStream_t stream);

@@ -289,8 +289,10 @@ class CachedDecoding:
         return self.model.decode(self.tokens, self.position, self.keys, self.values, span)
 
     def step(self, tokens):
+        """One decode step for `tokens` [rows] (None: already in self.tokens)."""
         span = self.span()
-        self.tokens.copy_(tokens)
+        if tokens is not None:
+            self.tokens.copy_(tokens)
         if self.keys.device.type != "cuda":
             logits = self._decode(span)
         else:
@@ -369,17 +371,18 @@ def stable_descending(values):
     return torch.sort(values, descending=True, stable=True)
 
 
-def multinomial_draws(probs, n):
+def multinomial_draws(probs, n, noise=None):
     """`torch.multinomial(probs, n)` without replacement as PyTorch computes
     it -- the exponential race: the n largest of probs / q with q ~ Exp(1)
     drawn from the default generator (argmax for n = 1) -- so the draws are
     the same, without its input checks (the max, min and sum of probs, read
     back to the host twice). `probs` here is a softmax output, finite and
     non-negative by construction; n < 1 goes to torch.multinomial, which
-    rejects it as the reference's call would."""
+    rejects it as the reference's call would. `noise`: the Exp(1) draws, if
+    the caller has made them already (`torch.empty_like(probs).exponential_()`)."""
     if n < 1:
         return torch.multinomial(probs, n)
-    q = torch.empty_like(probs).exponential_()
+    q = torch.empty_like(probs).exponential_() if noise is None else noise
     q = probs / q
     if n == 1:
         return torch.argmax(q, -1, keepdim=True)
@@ -442,30 +445,39 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
     `steps` decode steps. `on_prefill()` runs after the prefill and
     `on_step(i)` after decode step i.
 
-    The selection of the surviving beams (the reference's sort of the picked
-    scores, descending and stable) stays on the device: parents, tokens and
-    running scores are device tensors that feed the cache reorder, the
-    seen-token mask and the next step directly, so a step reads back only the
-    number of possible samples (`count_nonzero`, which the reference also
-    reads before sampling). The token sequences are rebuilt from the
-    per-step parents and tokens at the end.
-    Returns (best token sequence, per-step running scores)."""
+    The selection of the surviving beams stays on the device: parents,
+    tokens and running scores are device tensors that feed the cache
+    reorder, the seen-token mask and the next step directly, so a step reads
+    back only the number of possible samples (`count_nonzero`, which the
+    reference also reads before sampling). On the GPU one kernel
+    (`svq_beam_select`) makes the draws, the stable descending survivor
+    order, the parents and tokens and the next seen rows; the multinomial
+    sampling's Exp(1) draws come from the default generator before the host
+    read (nothing else draws in between, so the stream of draws is the same).
+    The token sequences are rebuilt from the per-step parents and tokens at
+    the end. Returns (best token sequence, per-step running scores)."""
     keep = 2 * beams
     capacity = capacity or embeddings.shape[1] + steps + 1
     decoding, logits = decoder.prefill(embeddings, beams, capacity)
     if on_prefill is not None:
         on_prefill()
     device, vocab = logits.device, logits.shape[-1]
+    on_gpu = device.type == "cuda"
     running_t = torch.tensor([0.0] + [-1e9] * (beams - 1), device=device)
-    seen = torch.zeros((beams, vocab), dtype=torch.bool, device=device)
+    # Two seen buffers (the next step's rows are gathered from the current
+    # ones), rows padded to 16 bytes for the selection kernel's copies.
+    pitch = (vocab + 15) // 16 * 16
+    seen_rows = [torch.zeros((beams, pitch), dtype=torch.bool, device=device) for _ in range(2)]
     beam_index = torch.arange(beams, device=device)
-    history = []
+    history = torch.empty((steps, 2, beams), dtype=torch.long, device=device)
     for step in range(steps):
-        penalized = penalize(torch.log_softmax(logits.float(), -1), seen)
+        seen_now, seen_next = seen_rows[step % 2], seen_rows[1 - step % 2]
+        penalized = penalize(torch.log_softmax(logits.float(), -1), seen_now[:, :vocab])
         log_probs, overflow, candidates = warp_candidates(penalized, temperature, top_p, 2,
                                                           with_index=True)
         scores = (log_probs + running_t[:, None]).view(1, -1)
         probs = scores.softmax(-1)
+        noise = torch.empty_like(probs).exponential_()
         # One host read for the sample count and the tie check. Only the
         # candidates can have a non-zero probability: count those.
         possible = torch.count_nonzero(probs.view(beams, vocab).gather(1, candidates))
@@ -475,31 +487,40 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
             scores = (log_probs + running_t[:, None]).view(1, -1)
             probs = scores.softmax(-1)
             possible = int(torch.count_nonzero(probs))
-        picks = multinomial_draws(probs, min(keep, possible))[0]
-        picked = scores[0].gather(0, picks)
-        # sorted(range(n), key=picked, reverse=True)[:beams]: descending, stable.
-        ordered, order = stable_descending(picked)
-        kept = min(beams, picks.numel())
-        chosen = picks[order[:kept]]
-        running_t = ordered[:kept]
-        if kept < beams:  # the reference repeats its best pick and scores the rest -1e9
-            chosen = torch.cat((chosen, chosen[:1].expand(beams - kept)))
-            running_t = torch.cat((running_t, torch.full((beams - kept,), -1e9, device=device)))
-        parents, tokens = chosen // vocab, chosen % vocab
-        history.append((parents, tokens))
-        seen = seen[parents]
-        seen[beam_index, tokens] = True
+        draws = min(keep, possible)
+        parents, tokens = history[step, 0], history[step, 1]
+        if on_gpu and not overflow and draws >= 1:
+            native.beam_select(probs, noise, scores, candidates, draws, seen_now, seen_next,
+                               running_t, parents, tokens, decoding.tokens)
+            next_tokens = None  # already in the step's input
+        else:
+            picks = multinomial_draws(probs, draws, noise)[0]
+            picked = scores[0].gather(0, picks)
+            # sorted(range(n), key=picked, reverse=True)[:beams]: descending, stable.
+            ordered, order = stable_descending(picked)
+            kept = min(beams, picks.numel())
+            chosen = picks[order[:kept]]
+            survivors = ordered[:kept]
+            if kept < beams:  # the reference repeats its best pick and scores the rest -1e9
+                chosen = torch.cat((chosen, chosen[:1].expand(beams - kept)))
+                survivors = torch.cat((survivors, torch.full((beams - kept,), -1e9, device=device)))
+            running_t.copy_(survivors)
+            parents.copy_(chosen // vocab)
+            tokens.copy_(chosen % vocab)
+            seen_next.copy_(seen_now[parents])
+            seen_next[beam_index, tokens] = True
+            next_tokens = tokens
         decoding.reorder_rows(parents)
-        logits = decoding.step(tokens)
+        logits = decoding.step(next_tokens)
         if on_step is not None:
             on_step(step + 1)
     # The token sequences: follow each final beam back through its parents.
-    if not history:
+    if not steps:
         return [], running_t.tolist()
-    parents_all = torch.stack([p for p, _ in history]).tolist()
-    tokens_all = torch.stack([t for _, t in history]).tolist()
+    parents_all = history[:, 0].tolist()
+    tokens_all = history[:, 1].tolist()
     beam, best = 0, []
-    for step in range(len(history) - 1, -1, -1):
+    for step in range(steps - 1, -1, -1):
         best.append(tokens_all[step][beam])
         beam = parents_all[step][beam]
     return best[::-1], running_t.tolist()

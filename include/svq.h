@@ -222,6 +222,35 @@ int svq_cache_reorder(uint16_t *cache, int64_t planes, int rows, int heads, int6
                       int head_dim, int64_t length, const int64_t *parents, void *stream);
 
 /*
+ * Survivor selection of one beam-sampling step once the number of draws is
+ * known (runtime_shared.py:233-262 without the finished-beam bookkeeping):
+ *   1. draws = torch.multinomial(probs, draws) without replacement, as
+ *      PyTorch computes it: the `draws` largest of probs / noise in
+ *      descending order (ties: the smaller flat index first), over the
+ *      candidate tokens only -- every other token must have probability 0;
+ *   2. survivors = the drawn flat indices sorted by scores[pick] descending
+ *      and stable, the first `beams` of them; when draws < beams the first
+ *      survivor fills the rest, with running score -1e9;
+ *   3. parents[b], tokens[b] = divmod(survivor b, vocab); running[b] =
+ *      scores[survivor b];
+ *   4. seen_out[b] = seen_in[parents[b]] with byte tokens[b] set to 1.
+ *   probs, noise, scores  fp32 [beams * vocab] (noise: Exp(1) draws, > 0)
+ *   candidates  int64 [beams, ncand]: token ids per beam, distinct per beam
+ *   seen_in, seen_out  bool (one byte) [beams, seen_pitch], distinct buffers,
+ *               16-byte aligned; seen_pitch >= vocab, a multiple of 16
+ *   running, parents, tokens  [beams] outputs; tokens_copy: a second copy of
+ *               tokens (e.g. the next step's input), or NULL
+ * beams <= 8, beams * ncand <= 1024, 1 <= draws <= min(2 * beams,
+ * beams * ncand). Asynchronous on `stream`; exact (one fp32 division per
+ * candidate, then comparisons and copies).
+ */
+int svq_beam_select(const float *probs, const float *noise, const float *scores,
+                    const int64_t *candidates, int beams, int64_t vocab, int ncand, int draws,
+                    const uint8_t *seen_in, uint8_t *seen_out, int64_t seen_pitch,
+                    float *running, int64_t *parents, int64_t *tokens, int64_t *tokens_copy,
+                    void *stream);
+
+/*
  * GGUF container reader (host memory; no GPU needed). Replaces the PyPI
  * `gguf` GGUFReader the reference opens its checkpoints with
  * (gguf_support.py:101-121): GGUF versions 2 and 3, memory-mapped once,

@@ -231,3 +231,28 @@ def test_gemv_split_workspace_size():
     assert lib.svq_gemv_split_workspace(5, 4608, 18432, 5) == 0  # m > 4
     assert lib.svq_gemv_split_workspace(2, 64, 40, 4) == -2
     assert lib.svq_gemv_split_workspace(2, 64, 64, 3) == -1
+
+
+def beam_select(**kw):
+    args = dict(probs=FAKE, noise=FAKE, scores=FAKE, candidates=FAKE, beams=2, vocab=320,
+                ncand=64, draws=4, seen_in=FAKE, seen_out=FAKE + 4096, pitch=320, running=FAKE,
+                parents=FAKE, tokens=FAKE, tokens_copy=None)
+    args.update(kw)
+    return native.load().svq_beam_select(
+        args["probs"], args["noise"], args["scores"], args["candidates"], args["beams"],
+        args["vocab"], args["ncand"], args["draws"], args["seen_in"], args["seen_out"],
+        args["pitch"], args["running"], args["parents"], args["tokens"], args["tokens_copy"],
+        None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(beams=0), -2), (dict(beams=9), -2), (dict(vocab=0), -2), (dict(ncand=0), -2),
+    (dict(ncand=321), -2), (dict(beams=8, ncand=129), -2), (dict(draws=0), -2),
+    (dict(draws=5), -2), (dict(beams=1, ncand=1, draws=2), -2), (dict(pitch=304), -2),
+    (dict(pitch=328), -2), (dict(probs=None), -3), (dict(seen_out=None), -3),
+    (dict(tokens=None), -3), (dict(candidates=FAKE + 4), -6), (dict(seen_in=FAKE + 8), -6),
+    (dict(tokens_copy=FAKE + 4), -6), (dict(seen_out=FAKE + 320), -2),  # overlaps seen_in
+])
+def test_beam_select_rejects_bad_arguments(kw, code):
+    assert beam_select(**kw) == code
+    assert native.load().svq_last_error().decode()
