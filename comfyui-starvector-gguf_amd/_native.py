@@ -74,8 +74,12 @@ def load() -> ctypes.CDLL:
         lib.svq_cache_reorder.argtypes = [vp, i64, i32, i32, i64, i32, i64, vp, vp]
         lib.svq_cache_reorder.restype = i32
         lib.svq_beam_select.argtypes = [vp, vp, vp, vp, i32, i64, i32, i32, vp, vp, i64, vp, vp,
-                                        vp, vp, vp]
+                                        vp, vp, i32, vp]
         lib.svq_beam_select.restype = i32
+        f32 = ctypes.c_float
+        lib.svq_beam_candidates.argtypes = [vp, vp, i64, vp, i32, i32, i32, i32, i32, f32, f32,
+                                            ctypes.c_double, vp, vp, vp, vp, vp]
+        lib.svq_beam_candidates.restype = i32
         cp = ctypes.c_char_p
         lib.svq_gguf_open.argtypes = [cp, i32, ctypes.POINTER(vp)]
         lib.svq_gguf_open.restype = i32
@@ -360,11 +364,14 @@ def beam_select(probs, noise, scores, candidates, draws, seen_in, seen_out, runn
     from probs (the exponential race with the given Exp(1) noise, over the
     candidate token ids [beams, ncand] only), the first `beams` of them by
     score (descending, stable), their parents and tokens, running scores, and
-    seen rows seen_out[b] = seen_in[parent b] with token b set. probs, noise
-    and scores are float32 with beams * vocab entries; seen_in / seen_out are
+    seen rows seen_out[b] = seen_in[parent b] with token b set. noise is
+    float32 with beams * vocab entries; probs and scores have as many, or one
+    per candidate (`beam_candidates`' outputs); seen_in / seen_out are
     distinct bool [beams, pitch] buffers, pitch >= vocab a multiple of 16."""
     lib = load()
     beams, ncand = candidates.shape
+    compact = probs.numel() == candidates.numel()
+    vocab = noise.numel() // beams
     tensors = (probs, noise, scores, candidates, seen_in, seen_out, running, parents, tokens) + (
         (tokens_copy,) if tokens_copy is not None else ())
     if any(not t.is_contiguous() or t.device != probs.device for t in tensors):
@@ -375,8 +382,10 @@ def beam_select(probs, noise, scores, candidates, draws, seen_in, seen_out, runn
         raise ValueError("candidates, parents and tokens must be int64")
     if seen_in.dtype != torch.bool or seen_out.dtype != torch.bool or seen_in.dim() != 2:
         raise ValueError("seen_in and seen_out must be bool [beams, pitch]")
-    if probs.numel() % beams or noise.numel() != probs.numel() or scores.numel() != probs.numel():
-        raise ValueError("probs, noise and scores must hold beams * vocab entries")
+    if noise.numel() % beams or scores.numel() != probs.numel() or (
+            not compact and probs.numel() != noise.numel()):
+        raise ValueError("noise must hold beams * vocab entries, probs and scores as many or "
+                         "one per candidate")
     if seen_out.shape != seen_in.shape or seen_in.shape[0] != beams:
         raise ValueError("seen_in and seen_out must be [beams, pitch]")
     if any(t.numel() != beams for t in (running, parents, tokens)):
@@ -384,11 +393,43 @@ def beam_select(probs, noise, scores, candidates, draws, seen_in, seen_out, runn
     with _on_device(probs.device):
         rc = lib.svq_beam_select(
             probs.data_ptr(), noise.data_ptr(), scores.data_ptr(), candidates.data_ptr(), beams,
-            probs.numel() // beams, ncand, int(draws), seen_in.data_ptr(), seen_out.data_ptr(),
+            vocab, ncand, int(draws), seen_in.data_ptr(), seen_out.data_ptr(),
             seen_in.shape[1], running.data_ptr(), parents.data_ptr(), tokens.data_ptr(),
-            tokens_copy.data_ptr() if tokens_copy is not None else None,
+            tokens_copy.data_ptr() if tokens_copy is not None else None, int(compact),
             _stream(probs.device))
     _check(lib, "svq_beam_select", rc)
+
+
+def beam_candidates(logits, seen, running, k, kc, keep, penalty, temperature, top_p,
+                    candidates, scores, probs, status) -> None:
+    """Candidates of a beam-sampling step (svq_beam_candidates) on the
+    device, asynchronously: from fp16 logits [beams, vocab], the seen rows
+    (bool [beams, pitch]) and running scores, each row's kc largest warped
+    log-probabilities (token ids into `candidates` [beams, kc] int64, value +
+    running score into `scores` [beams, kc] float32), their joint softmax
+    (`probs`, float32 [beams * kc]) and `status` (int64 [2 + beams]: number
+    of non-zero probs, overflow flag, flag per row)."""
+    lib = load()
+    beams, vocab = logits.shape
+    tensors = (logits, seen, running, candidates, scores, probs, status)
+    if any(not t.is_contiguous() or t.device != logits.device for t in tensors):
+        raise ValueError("beam_candidates tensors must be contiguous and on one device")
+    if logits.dtype != torch.float16 or seen.dtype != torch.bool or seen.dim() != 2 or \
+            seen.shape[0] != beams:
+        raise ValueError("logits must be float16 [beams, vocab] and seen bool [beams, pitch]")
+    if candidates.dtype != torch.int64 or status.dtype != torch.int64 or any(
+            t.dtype != torch.float32 for t in (running, scores, probs)):
+        raise ValueError("candidates and status must be int64; running, scores and probs float32")
+    if candidates.shape != (beams, kc) or scores.numel() != beams * kc or \
+            probs.numel() != beams * kc or status.numel() != 2 + beams or running.numel() != beams:
+        raise ValueError("output shapes do not match beams and kc")
+    with _on_device(logits.device):
+        rc = lib.svq_beam_candidates(
+            logits.data_ptr(), seen.data_ptr(), seen.shape[1], running.data_ptr(), beams, vocab,
+            int(k), int(kc), int(keep), float(penalty), float(temperature), float(top_p),
+            candidates.data_ptr(), scores.data_ptr(), probs.data_ptr(), status.data_ptr(),
+            _stream(logits.device))
+    _check(lib, "svq_beam_candidates", rc)
 
 
 def pack_soa(aos_ptr: int, nblocks: int, qtype: str, q: torch.Tensor, s: torch.Tensor,

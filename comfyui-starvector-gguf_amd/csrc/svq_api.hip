@@ -680,7 +680,7 @@ int svq_beam_select(const float* probs, const float* noise, const float* scores,
                     const int64_t* candidates, int beams, int64_t vocab, int ncand, int draws,
                     const uint8_t* seen_in, uint8_t* seen_out, int64_t seen_pitch,
                     float* running, int64_t* parents, int64_t* tokens, int64_t* tokens_copy,
-                    void* stream) {
+                    int compact, void* stream) {
   if (beams < 1 || beams > svq::kBeamMaxRows || vocab < 1 || ncand < 1 || ncand > vocab ||
       (int64_t)beams * ncand > svq::kBeamMaxCandidates || draws < 1 || draws > 2 * beams ||
       draws > beams * ncand || seen_pitch < vocab || seen_pitch % 16 != 0)
@@ -703,9 +703,53 @@ int svq_beam_select(const float* probs, const float* noise, const float* scores,
     return fail(SVQ_E_SHAPE, "seen_in and seen_out overlap");
   svq::BeamSelectArgs a{probs,   noise,       scores, candidates, seen_in, seen_out,
                         seen_pitch, running, parents, tokens,     tokens_copy, vocab,
-                        beams,   ncand,       draws};
+                        beams,   ncand,       draws,  compact != 0};
+  if (compact && ncand > svq::kCandMax)
+    return fail(SVQ_E_SHAPE, "compact beam selection takes at most %d candidates per beam",
+                svq::kCandMax);
   const hipError_t e = svq::launch_beam_select(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "svq_beam_select launch");
+  return 0;
+}
+
+int svq_beam_candidates(const uint16_t* logits, const uint8_t* seen, int64_t seen_pitch,
+                        const float* running, int beams, int vocab, int k, int kc, int keep,
+                        float penalty, float temperature, double top_p, int64_t* candidates,
+                        float* scores, float* probs, int64_t* status, void* stream) {
+  if (beams < 1 || beams > svq::kBeamMaxRows || vocab < 1 || vocab > svq::kCandMaxVocab ||
+      k < 1 || kc < k || kc > svq::kCandMax || kc > vocab || keep < 0 || keep > kc ||
+      seen_pitch < vocab || seen_pitch % 16 != 0)
+    return fail(SVQ_E_SHAPE,
+                "invalid beam candidates beams=%d vocab=%d k=%d kc=%d keep=%d seen_pitch=%lld",
+                beams, vocab, k, kc, keep, (long long)seen_pitch);
+  if (!(temperature > 0.0f) || !(penalty > 0.0f) || !(top_p >= 0.0 && top_p <= 1.0))
+    return fail(SVQ_E_SHAPE, "invalid temperature %g, penalty %g or top_p %g",
+                (double)temperature, (double)penalty, (double)top_p);
+  if (!logits || !seen || !running || !candidates || !scores || !probs || !status)
+    return fail(SVQ_E_NULL, "NULL beam candidates argument");
+  if (!aligned(logits, 2) || !aligned(running, 4) || !aligned(candidates, 8) ||
+      !aligned(scores, 4) || !aligned(probs, 4) || !aligned(status, 8))
+    return fail(SVQ_E_ALIGN, "misaligned beam candidates argument");
+  svq::BeamCandArgs a{};
+  a.logits = logits;
+  a.seen = seen;
+  a.seen_pitch = seen_pitch;
+  a.running = running;
+  a.candidates = candidates;
+  a.scores = scores;
+  a.probs = probs;
+  a.status = status;
+  a.vocab = vocab;
+  a.beams = beams;
+  a.k = k;
+  a.kc = kc;
+  a.keep = keep;
+  a.penalty = penalty;
+  a.temperature = temperature;
+  a.top_p_cut = (float)(1.0 - top_p);  // torch compares with the fp32 rounding of 1 - top_p
+  a.use_top_p = top_p < 1.0;
+  const hipError_t e = svq::launch_beam_candidates(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "svq_beam_candidates launch");
   return 0;
 }
 

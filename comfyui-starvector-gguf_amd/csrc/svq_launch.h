@@ -137,8 +137,33 @@ struct BeamSelectArgs {
   int beams;
   int ncand;
   int draws;
+  int compact;                // probs / scores are [beams, ncand] (per candidate)
 };
 hipError_t launch_beam_select(const BeamSelectArgs& a, hipStream_t stream);
+
+// Candidate tokens of a beam-sampling step (svq_beam_candidates).
+constexpr int kCandMaxVocab = 65536;
+constexpr int kCandMax = 64;  // candidates per row
+struct BeamCandArgs {
+  const uint16_t* logits;  // fp16 [beams, vocab]
+  const uint8_t* seen;     // [beams, seen_pitch]
+  int64_t seen_pitch;
+  const float* running;    // [beams]
+  int64_t* candidates;     // [beams, kc] out
+  float* scores;           // [beams, kc] out
+  float* probs;            // [beams * kc] out
+  int64_t* status;         // [2 + beams] out: draws possible, any overflow, overflow per row
+  int vocab;
+  int beams;
+  int k;
+  int kc;
+  int keep;
+  float penalty;
+  float temperature;
+  float top_p_cut;         // 1 - top_p
+  int use_top_p;
+};
+hipError_t launch_beam_candidates(const BeamCandArgs& a, hipStream_t stream);
 
 hipError_t launch_dequant(const uint8_t* q, const uint16_t* s, void* out,
                           int64_t nblocks, int qtype, int out_dtype,

@@ -449,11 +449,15 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
     tokens and running scores are device tensors that feed the cache
     reorder, the seen-token mask and the next step directly, so a step reads
     back only the number of possible samples (`count_nonzero`, which the
-    reference also reads before sampling). On the GPU one kernel
-    (`svq_beam_select`) makes the draws, the stable descending survivor
-    order, the parents and tokens and the next seen rows; the multinomial
-    sampling's Exp(1) draws come from the default generator before the host
-    read (nothing else draws in between, so the stream of draws is the same).
+    reference also reads before sampling). On the GPU two kernels
+    (`svq_beam_candidates`) form each row's candidates, scores and joint
+    probabilities from the logits -- their sums add in another order than
+    torch's reductions, so scores agree with the torch formulation to
+    rounding -- and one (`svq_beam_select`) makes the draws, the stable
+    descending survivor order, the parents and tokens and the next seen rows;
+    the multinomial sampling's Exp(1) draws come from the default generator
+    before the host read (nothing else draws in between, so the stream of
+    draws is the same).
     The token sequences are rebuilt from the per-step parents and tokens at
     the end. Returns (best token sequence, per-step running scores)."""
     keep = 2 * beams
@@ -470,19 +474,38 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
     seen_rows = [torch.zeros((beams, pitch), dtype=torch.bool, device=device) for _ in range(2)]
     beam_index = torch.arange(beams, device=device)
     history = torch.empty((steps, 2, beams), dtype=torch.long, device=device)
+    # On the GPU the candidates come from one kernel pair (svq_beam_candidates)
+    # when the top-k candidate set fits it.
+    k = max(TOP_K, 2)
+    kc = min(k + TIE_ROOM, vocab)
+    fused = on_gpu and k <= kc <= 64 and vocab <= 65536 and beams <= 8 and \
+        logits.dtype == torch.float16
+    if fused:
+        cand = torch.empty((beams, kc), dtype=torch.long, device=device)
+        cand_scores = torch.empty((beams, kc), device=device)
+        cand_probs = torch.empty(beams * kc, device=device)
+        status = torch.empty(2 + beams, dtype=torch.long, device=device)
     for step in range(steps):
         seen_now, seen_next = seen_rows[step % 2], seen_rows[1 - step % 2]
-        penalized = penalize(torch.log_softmax(logits.float(), -1), seen_now[:, :vocab])
-        log_probs, overflow, candidates = warp_candidates(penalized, temperature, top_p, 2,
-                                                          with_index=True)
-        scores = (log_probs + running_t[:, None]).view(1, -1)
-        probs = scores.softmax(-1)
-        noise = torch.empty_like(probs).exponential_()
-        # One host read for the sample count and the tie check. Only the
-        # candidates can have a non-zero probability: count those.
-        possible = torch.count_nonzero(probs.view(beams, vocab).gather(1, candidates))
-        possible, overflow = torch.stack((possible, overflow.long())).tolist()
+        if fused:
+            native.beam_candidates(logits.contiguous(), seen_now, running_t, k, kc, 2,
+                                   REPETITION_PENALTY, temperature, top_p, cand, cand_scores,
+                                   cand_probs, status)
+            noise = torch.empty((1, beams * vocab), device=device).exponential_()
+            possible, overflow = status[:2].tolist()
+        else:
+            penalized = penalize(torch.log_softmax(logits.float(), -1), seen_now[:, :vocab])
+            log_probs, overflow, candidates = warp_candidates(penalized, temperature, top_p, 2,
+                                                              with_index=True)
+            scores = (log_probs + running_t[:, None]).view(1, -1)
+            probs = scores.softmax(-1)
+            noise = torch.empty_like(probs).exponential_()
+            # One host read for the sample count and the tie check. Only the
+            # candidates can have a non-zero probability: count those.
+            possible = torch.count_nonzero(probs.view(beams, vocab).gather(1, candidates))
+            possible, overflow = torch.stack((possible, overflow.long())).tolist()
         if overflow:
+            penalized = penalize(torch.log_softmax(logits.float(), -1), seen_now[:, :vocab])
             log_probs = warp(penalized, temperature, top_p, 2)
             scores = (log_probs + running_t[:, None]).view(1, -1)
             probs = scores.softmax(-1)
@@ -490,8 +513,12 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
         draws = min(keep, possible)
         parents, tokens = history[step, 0], history[step, 1]
         if on_gpu and not overflow and draws >= 1:
-            native.beam_select(probs, noise, scores, candidates, draws, seen_now, seen_next,
-                               running_t, parents, tokens, decoding.tokens)
+            if fused:
+                native.beam_select(cand_probs, noise, cand_scores, cand, draws, seen_now,
+                                   seen_next, running_t, parents, tokens, decoding.tokens)
+            else:
+                native.beam_select(probs, noise, scores, candidates, draws, seen_now, seen_next,
+                                   running_t, parents, tokens, decoding.tokens)
             next_tokens = None  # already in the step's input
         else:
             picks = multinomial_draws(probs, draws, noise)[0]

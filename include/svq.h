@@ -240,6 +240,9 @@ int svq_cache_reorder(uint16_t *cache, int64_t planes, int rows, int heads, int6
  *               16-byte aligned; seen_pitch >= vocab, a multiple of 16
  *   running, parents, tokens  [beams] outputs; tokens_copy: a second copy of
  *               tokens (e.g. the next step's input), or NULL
+ *   compact     0: probs and scores are [beams * vocab]; 1: they are
+ *               [beams, ncand] per candidate (svq_beam_candidates' outputs,
+ *               ncand <= 64); noise is [beams * vocab] either way
  * beams <= 8, beams * ncand <= 1024, 1 <= draws <= min(2 * beams,
  * beams * ncand). Asynchronous on `stream`; exact (one fp32 division per
  * candidate, then comparisons and copies).
@@ -248,7 +251,39 @@ int svq_beam_select(const float *probs, const float *noise, const float *scores,
                     const int64_t *candidates, int beams, int64_t vocab, int ncand, int draws,
                     const uint8_t *seen_in, uint8_t *seen_out, int64_t seen_pitch,
                     float *running, int64_t *parents, int64_t *tokens, int64_t *tokens_copy,
-                    void *stream);
+                    int compact, void *stream);
+
+/*
+ * Candidates of one beam-sampling step (runtime_shared.py:228-231), on each
+ * beam row's kc largest warped log-probabilities instead of the whole
+ * vocabulary: log_softmax of the fp16 logits in fp32, the repetition
+ * penalty on seen tokens (v < 0 ? v * penalty : v / penalty), division by
+ * the temperature (skipped at 1), top-k (every value below the k-th largest
+ * becomes -inf), top-p over the kc values (softmax, sums from the smallest
+ * up, removal where the sum <= 1 - top_p except the `keep` largest), plus
+ * the beam's running score; then the softmax over all beams' candidates
+ * jointly (the reference's softmax over the flattened [1, beams * vocab]
+ * scores, whose other entries are -inf).
+ *   logits      fp16 [beams, vocab]
+ *   seen        bool [beams, seen_pitch]; seen_pitch >= vocab, a multiple of 16
+ *   running     fp32 [beams]
+ *   candidates  int64 [beams, kc] out: token ids, value descending, token ascending
+ *   scores      fp32 [beams, kc] out: warped log-prob + running (-inf if removed)
+ *   probs       fp32 [beams * kc] out: joint softmax of scores
+ *   status      int64 [2 + beams] out: number of non-zero probs; 1 if any row
+ *               overflows (more than 1024 values tie with its kc-th largest, or
+ *               its kc-th largest equals its k-th: the candidates may then miss
+ *               tokens the reference keeps, and the caller must warp the whole
+ *               vocabulary); then the flag per row
+ * beams <= 8, vocab <= 65536, 1 <= k <= kc <= min(64, vocab), keep <= kc.
+ * Sums add in another order than torch's reductions: results agree with the
+ * reference's to rounding. Asynchronous on `stream`; svq_beam_select with
+ * compact = 1 draws from these outputs.
+ */
+int svq_beam_candidates(const uint16_t *logits, const uint8_t *seen, int64_t seen_pitch,
+                        const float *running, int beams, int vocab, int k, int kc, int keep,
+                        float penalty, float temperature, double top_p, int64_t *candidates,
+                        float *scores, float *probs, int64_t *status, void *stream);
 
 /*
  * GGUF container reader (host memory; no GPU needed). Replaces the PyPI

@@ -242,7 +242,7 @@ def beam_select(**kw):
         args["probs"], args["noise"], args["scores"], args["candidates"], args["beams"],
         args["vocab"], args["ncand"], args["draws"], args["seen_in"], args["seen_out"],
         args["pitch"], args["running"], args["parents"], args["tokens"], args["tokens_copy"],
-        None)
+        args.get("compact", 0), None)
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -252,7 +252,33 @@ def beam_select(**kw):
     (dict(pitch=328), -2), (dict(probs=None), -3), (dict(seen_out=None), -3),
     (dict(tokens=None), -3), (dict(candidates=FAKE + 4), -6), (dict(seen_in=FAKE + 8), -6),
     (dict(tokens_copy=FAKE + 4), -6), (dict(seen_out=FAKE + 320), -2),  # overlaps seen_in
+    (dict(beams=1, ncand=65, draws=2, compact=1), -2),
 ])
 def test_beam_select_rejects_bad_arguments(kw, code):
     assert beam_select(**kw) == code
+    assert native.load().svq_last_error().decode()
+
+
+def beam_candidates(**kw):
+    args = dict(logits=FAKE, seen=FAKE, pitch=320, running=FAKE, beams=2, vocab=320, k=50, kc=64,
+                keep=2, penalty=3.1, temperature=1.5, top_p=0.9, candidates=FAKE, scores=FAKE,
+                probs=FAKE, status=FAKE)
+    args.update(kw)
+    return native.load().svq_beam_candidates(
+        args["logits"], args["seen"], args["pitch"], args["running"], args["beams"],
+        args["vocab"], args["k"], args["kc"], args["keep"], args["penalty"],
+        args["temperature"], args["top_p"], args["candidates"], args["scores"], args["probs"],
+        args["status"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(beams=0), -2), (dict(beams=9), -2), (dict(vocab=65537, pitch=65552), -2),
+    (dict(k=0), -2), (dict(k=65, kc=64), -2), (dict(kc=65), -2), (dict(vocab=60, pitch=64), -2),
+    (dict(keep=65), -2), (dict(keep=-1), -2), (dict(pitch=304), -2), (dict(pitch=328), -2),
+    (dict(temperature=0.0), -2), (dict(penalty=-1.0), -2), (dict(top_p=1.5), -2),
+    (dict(logits=None), -3), (dict(status=None), -3), (dict(logits=FAKE + 1), -6),
+    (dict(candidates=FAKE + 4), -6), (dict(status=FAKE + 4), -6),
+])
+def test_beam_candidates_rejects_bad_arguments(kw, code):
+    assert beam_candidates(**kw) == code
     assert native.load().svq_last_error().decode()

@@ -240,8 +240,9 @@ def test_beam_steps_matches_host_selection_cpu():
 
 @pytest.mark.gpu
 def test_beam_steps_matches_host_selection_gpu(cuda_device):
-    """The same on the GPU: the svq_cache_reorder kernel and graph-replayed
-    steps against host-chosen parents and torch slice copies."""
+    """The same on the GPU: the candidate and selection kernels, the
+    svq_cache_reorder kernel and graph-replayed steps against torch warpers,
+    torch.multinomial, host-chosen parents and torch slice copies."""
     model = small_model(cuda_device)
     emb = prompt(9, cuda_device, torch.float16)
     with torch.inference_mode():
@@ -249,7 +250,10 @@ def test_beam_steps_matches_host_selection_gpu(cuda_device):
         want = beam_steps_host_selection(model, emb, 8, beams=2)
         torch.manual_seed(5)
         got = beam_steps(model, emb, 8, beams=2)
-    assert got[0] == want[0] and got[1] == want[1], (got, want)
+    # The candidate kernels' sums add in another order than torch's: the
+    # running scores agree to rounding, the tokens exactly.
+    assert got[0] == want[0], (got, want)
+    torch.testing.assert_close(torch.tensor(got[1]), torch.tensor(want[1]), rtol=1e-5, atol=1e-4)
 
 
 @pytest.mark.parametrize("values", ([3.0, 1.0, 3.0, 2.0], [1.0, 1.0, 1.0, 1.0], [0.5],

@@ -149,3 +149,99 @@ def test_beam_select_rejects_mismatched_tensors(cuda_device):
         native.beam_select(probs, noise, scores, candidates, 4, seen, out[:1], f, i, i)
     with pytest.raises(native.SVQError):
         native.beam_select(probs, noise, scores, candidates, 5, seen, out, f, i, i)
+
+
+# --- svq_beam_candidates against the torch formulation of the warpers ---
+
+from starvector_amd import decoder  # noqa: E402
+
+
+def torch_candidates(logits, seen, running, temperature, top_p, keep=2):
+    beams, vocab = logits.shape
+    penalized = decoder.penalize(torch.log_softmax(logits.float(), -1), seen[:, :vocab])
+    log_probs, overflow, index = decoder.warp_candidates(penalized, temperature, top_p, keep,
+                                                         with_index=True)
+    scores = (log_probs + running[:, None]).view(1, -1)
+    probs = scores.softmax(-1)
+    count = torch.count_nonzero(probs.view(beams, vocab).gather(1, index))
+    return scores.view(beams, vocab), probs.view(beams, vocab), int(count), bool(overflow)
+
+
+def run_candidates(logits, seen, running, temperature, top_p, keep=2):
+    beams, vocab = logits.shape
+    k = max(decoder.TOP_K, keep)
+    kc = min(k + decoder.TIE_ROOM, vocab)
+    dev = logits.device
+    cand = torch.full((beams, kc), -7, dtype=torch.long, device=dev)
+    scores = torch.full((beams, kc), 7.0, device=dev)
+    probs = torch.full((beams * kc,), 7.0, device=dev)
+    status = torch.full((2 + beams,), -7, dtype=torch.long, device=dev)
+    native.beam_candidates(logits, seen, running, k, kc, keep, decoder.REPETITION_PENALTY,
+                           temperature, top_p, cand, scores, probs, status)
+    torch.cuda.synchronize()
+    return cand, scores, probs.view(beams, kc), status
+
+
+def logits_case(device, beams, vocab, seed, ties=False, seen_rate=0.05):
+    g = torch.Generator(device=device).manual_seed(seed)
+    logits = torch.randn((beams, vocab), generator=g, device=device) * 3
+    if ties:
+        logits = torch.round(logits)
+    pitch = (vocab + 15) // 16 * 16
+    seen = torch.rand((beams, pitch), generator=g, device=device) < seen_rate
+    # Seen tokens among the top ones, so the penalty reorders the top-k.
+    top = torch.topk(logits, 8).indices
+    seen.scatter_(1, top[:, ::2], True)
+    running = torch.randn(beams, generator=g, device=device) * 4
+    return logits.half(), seen, running
+
+
+CAND_CASES = [
+    # beams, vocab, temperature, top_p
+    (1, 320, 1.0, 1.0),
+    (2, 320, 1.5, 0.9),
+    (2, 1001, 1.5, 0.9),
+    (2, 49152, 1.5, 0.9),
+    (2, 49157, 0.7, 0.5),
+    (4, 4096, 1.0, 0.9),
+    (8, 49152, 1.5, 0.95),
+    (3, 65536, 1.5, 0.9),
+]
+
+
+@pytest.mark.parametrize("beams,vocab,temperature,top_p", CAND_CASES)
+@pytest.mark.parametrize("seed", (1, 2))
+def test_beam_candidates_match_torch(cuda_device, beams, vocab, temperature, top_p, seed):
+    logits, seen, running = logits_case(cuda_device, beams, vocab, seed)
+    if beams > 1:
+        running[1] = -1e9  # a dead beam, as in the first steps
+    want_scores, want_probs, want_count, want_overflow = torch_candidates(
+        logits, seen, running, temperature, top_p)
+    cand, scores, probs, status = run_candidates(logits, seen, running, temperature, top_p)
+    assert bool(status[1]) == want_overflow is False
+    assert int(status[0]) == want_count
+    for r in range(beams):
+        got_s, got_p = scores[r], probs[r]
+        ws = want_scores[r].gather(0, cand[r])
+        wp = want_probs[r].gather(0, cand[r])
+        # Same kept tokens (finite scores), scores and probabilities to rounding.
+        assert torch.equal(torch.isfinite(got_s), torch.isfinite(ws))
+        assert int(torch.isfinite(got_s).sum()) == int(torch.isfinite(want_scores[r]).sum())
+        fin = torch.isfinite(ws)
+        torch.testing.assert_close(got_s[fin], ws[fin], rtol=1e-6, atol=1e-5)
+        torch.testing.assert_close(got_p, wp, rtol=1e-5, atol=1e-7)
+        # Candidates are distinct, in range, and their warped values descend.
+        assert cand[r].unique().numel() == cand.shape[1]
+        assert int(cand[r].min()) >= 0 and int(cand[r].max()) < vocab
+        vals = (scores[r] - running[r])[fin]
+        assert bool((vals[1:] <= vals[:-1]).all())
+
+
+def test_beam_candidates_report_tie_overflow(cuda_device):
+    """Rounded logits tie at the top-k threshold beyond the candidate room:
+    both forms report the overflow."""
+    logits, seen, running = logits_case(cuda_device, 2, 49152, 3, ties=True, seen_rate=0.0)
+    want = torch_candidates(logits, seen, running, 1.5, 0.9)
+    _, _, _, status = run_candidates(logits, seen, running, 1.5, 0.9)
+    assert want[3] is True
+    assert bool(status[1]) and (bool(status[2]) or bool(status[3]))
