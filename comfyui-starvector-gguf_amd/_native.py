@@ -78,8 +78,10 @@ def load() -> ctypes.CDLL:
         lib.svq_beam_select.restype = i32
         f32 = ctypes.c_float
         lib.svq_beam_candidates.argtypes = [vp, vp, i64, vp, i32, i32, i32, i32, i32, f32, f32,
-                                            ctypes.c_double, vp, vp, vp, vp, vp]
+                                            ctypes.c_double, vp, vp, vp, vp, vp, i64, vp]
         lib.svq_beam_candidates.restype = i32
+        lib.svq_beam_candidates_workspace.argtypes = [i32, i32, i32]
+        lib.svq_beam_candidates_workspace.restype = i64
         cp = ctypes.c_char_p
         lib.svq_gguf_open.argtypes = [cp, i32, ctypes.POINTER(vp)]
         lib.svq_gguf_open.restype = i32
@@ -400,8 +402,16 @@ def beam_select(probs, noise, scores, candidates, draws, seen_in, seen_out, runn
     _check(lib, "svq_beam_select", rc)
 
 
+def beam_candidates_workspace(beams: int, vocab: int, kc: int, device) -> torch.Tensor:
+    """A workspace for `beam_candidates` (uint8, written and read within a call)."""
+    lib = load()
+    need = lib.svq_beam_candidates_workspace(beams, vocab, kc)
+    _check(lib, "svq_beam_candidates_workspace", min(need, 0))
+    return torch.empty(need, dtype=torch.uint8, device=device)
+
+
 def beam_candidates(logits, seen, running, k, kc, keep, penalty, temperature, top_p,
-                    candidates, scores, probs, status) -> None:
+                    candidates, scores, probs, status, workspace) -> None:
     """Candidates of a beam-sampling step (svq_beam_candidates) on the
     device, asynchronously: from fp16 logits [beams, vocab], the seen rows
     (bool [beams, pitch]) and running scores, each row's kc largest warped
@@ -411,7 +421,7 @@ def beam_candidates(logits, seen, running, k, kc, keep, penalty, temperature, to
     of non-zero probs, overflow flag, flag per row)."""
     lib = load()
     beams, vocab = logits.shape
-    tensors = (logits, seen, running, candidates, scores, probs, status)
+    tensors = (logits, seen, running, candidates, scores, probs, status, workspace)
     if any(not t.is_contiguous() or t.device != logits.device for t in tensors):
         raise ValueError("beam_candidates tensors must be contiguous and on one device")
     if logits.dtype != torch.float16 or seen.dtype != torch.bool or seen.dim() != 2 or \
@@ -428,6 +438,7 @@ def beam_candidates(logits, seen, running, k, kc, keep, penalty, temperature, to
             logits.data_ptr(), seen.data_ptr(), seen.shape[1], running.data_ptr(), beams, vocab,
             int(k), int(kc), int(keep), float(penalty), float(temperature), float(top_p),
             candidates.data_ptr(), scores.data_ptr(), probs.data_ptr(), status.data_ptr(),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(),
             _stream(logits.device))
     _check(lib, "svq_beam_candidates", rc)
 

@@ -712,10 +712,18 @@ int svq_beam_select(const float* probs, const float* noise, const float* scores,
   return 0;
 }
 
+int64_t svq_beam_candidates_workspace(int beams, int vocab, int kc) {
+  if (beams < 1 || beams > svq::kBeamMaxRows || vocab < 1 || vocab > svq::kCandMaxVocab ||
+      kc < 1 || kc > svq::kCandMax || kc > vocab)
+    return fail(SVQ_E_SHAPE, "invalid beam candidates beams=%d vocab=%d kc=%d", beams, vocab, kc);
+  return svq::beam_candidates_workspace(beams, vocab, kc);
+}
+
 int svq_beam_candidates(const uint16_t* logits, const uint8_t* seen, int64_t seen_pitch,
                         const float* running, int beams, int vocab, int k, int kc, int keep,
                         float penalty, float temperature, double top_p, int64_t* candidates,
-                        float* scores, float* probs, int64_t* status, void* stream) {
+                        float* scores, float* probs, int64_t* status, void* workspace,
+                        int64_t workspace_bytes, void* stream) {
   if (beams < 1 || beams > svq::kBeamMaxRows || vocab < 1 || vocab > svq::kCandMaxVocab ||
       k < 1 || kc < k || kc > svq::kCandMax || kc > vocab || keep < 0 || keep > kc ||
       seen_pitch < vocab || seen_pitch % 16 != 0)
@@ -725,11 +733,15 @@ int svq_beam_candidates(const uint16_t* logits, const uint8_t* seen, int64_t see
   if (!(temperature > 0.0f) || !(penalty > 0.0f) || !(top_p >= 0.0 && top_p <= 1.0))
     return fail(SVQ_E_SHAPE, "invalid temperature %g, penalty %g or top_p %g",
                 (double)temperature, (double)penalty, (double)top_p);
-  if (!logits || !seen || !running || !candidates || !scores || !probs || !status)
+  if (!logits || !seen || !running || !candidates || !scores || !probs || !status || !workspace)
     return fail(SVQ_E_NULL, "NULL beam candidates argument");
   if (!aligned(logits, 2) || !aligned(running, 4) || !aligned(candidates, 8) ||
-      !aligned(scores, 4) || !aligned(probs, 4) || !aligned(status, 8))
+      !aligned(scores, 4) || !aligned(probs, 4) || !aligned(status, 8) || !aligned(workspace, 8))
     return fail(SVQ_E_ALIGN, "misaligned beam candidates argument");
+  const int64_t need = svq::beam_candidates_workspace(beams, vocab, kc);
+  if (workspace_bytes < need)
+    return fail(SVQ_E_WORKSPACE, "workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)need);
   svq::BeamCandArgs a{};
   a.logits = logits;
   a.seen = seen;
@@ -748,6 +760,7 @@ int svq_beam_candidates(const uint16_t* logits, const uint8_t* seen, int64_t see
   a.temperature = temperature;
   a.top_p_cut = (float)(1.0 - top_p);  // torch compares with the fp32 rounding of 1 - top_p
   a.use_top_p = top_p < 1.0;
+  a.workspace = workspace;
   const hipError_t e = svq::launch_beam_candidates(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "svq_beam_candidates launch");
   return 0;

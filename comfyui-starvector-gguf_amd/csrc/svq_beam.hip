@@ -160,39 +160,43 @@ __global__ __launch_bounds__(kThreads) void beam_select_kernel(BeamSelectArgs a)
 // Candidates of a beam-sampling step (runtime_shared.py:228-231: log-softmax,
 // repetition penalty, temperature, top-k and top-p warpers, running scores
 // and the joint softmax over all beams), computed on each row's kc largest
-// warped log-probabilities instead of the whole vocabulary. Kernel 1 (one
-// workgroup per beam row) keeps the row's fp16 logits in registers (64 per
-// thread) and forms
-//   log_softmax(x) = (x - max) - log(sum exp(x - max))  (expf / logf);
+// warped log-probabilities instead of the whole vocabulary:
+//   lp = log_softmax(x) = (x - max) - log(sum exp(x - max))  (expf / logf);
 //   w = penalty: seen ? (lp < 0 ? lp * p : lp / p) : lp;  v = w / t
 //   (temperature t; no division at t = 1).
-// The kc largest are found on w (v is monotone in w, so the order agrees;
-// ties that the division creates at the kc-th value only matter where that
-// value is also the k-th, which is reported as overflow): a 4-pass radix
-// select on order-preserving keys (wave-aggregated LDS histograms), then
-// every entry at or above the kc-th largest is sorted on v (descending,
-// token ascending). Top-k: values below the k-th largest become -inf. Top-p
-// over the kc values: softmax, sums from the smallest up, removal where the
-// sum <= 1 - top_p except the `keep` largest. Candidate score = v +
-// running[row]. Kernel 2 (one workgroup) makes the joint softmax over all
-// candidates, the number of non-zero probabilities and the overflow flag.
+// w is increasing in x among the unseen tokens and among the seen ones, so
+// the kc largest w lie among the kc largest x of each class, and v is
+// monotone in w (ties that the division creates at the kc-th value only
+// matter where that value is also the k-th, which is reported as overflow).
+// 1. Slice kernel (16 slices of 4096 tokens per row at most, 256 threads):
+//    the slice's max and sum of exp(x - max), and its kc largest x among
+//    unseen and among seen tokens (radix select on order-preserving keys;
+//    ties at the cut keep the first in thread order).
+// 2. Merge kernel (one workgroup per row): the row's max and log-sum from
+//    the slices' (rescaled in slice order), w and v of every kept entry, the
+//    kc largest w, sorted on v descending (token ascending); top-k: values
+//    below the k-th become -inf; top-p over the kc values: softmax, sums
+//    from the smallest up, removal where the sum <= 1 - top_p except the
+//    `keep` largest; candidate score = v + running[row].
+// 3. Joint kernel (one workgroup): softmax over all candidates of all rows,
+//    the number of non-zero probabilities and the overflow flag.
 // The sums add in another order than torch's reductions (the results agree
 // to rounding); comparisons, the penalty, the temperature and the score
 // additions are the same fp32 operations.
+constexpr int kSliceThreads = 256;
+constexpr int kSliceJ = 16;                          // tokens per thread
+constexpr int kSliceLen = kSliceThreads * kSliceJ;   // 4096
+constexpr int kMaxSlices = kCandMaxVocab / kSliceLen;  // 16
 constexpr int kCandThreads = 1024;
-constexpr int kCandPerThread = kCandMaxVocab / kCandThreads;  // 64, as fp16 pairs
-constexpr int kCandCap = 1024;  // entries >= the kc-th largest kept for the sort
-constexpr int kCandWaves = kCandThreads / 64;
+constexpr int kMergeJ = 2 * kMaxSlices * kCandMax / kCandThreads;  // entries per thread: 2
 
 __device__ __forceinline__ uint32_t order_key(float v) {
   const uint32_t b = __float_as_uint(v);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
-__device__ __forceinline__ float key_value(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
 
-// Block-wide max / sum over kCandThreads threads, the same order every call.
+// Block-wide max / sum over T threads, the same order every call.
+template <int T>
 __device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
@@ -204,89 +208,49 @@ __device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) 
   if (lane == 0) red[w] = v;
   __syncthreads();
   float r = red[0];
-  for (int i = 1; i < kCandWaves; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
+  for (int i = 1; i < T / 64; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
   return r;
 }
 
-__global__ __launch_bounds__(kCandThreads) void beam_candidates_kernel(BeamCandArgs a) {
-  __shared__ float red[kCandWaves];
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t pick[2];  // digit, entries above it
-  __shared__ int count;
-  __shared__ float lv[kCandCap];
-  __shared__ int li[kCandCap];
-  __shared__ float sv[kCandMax];
-  __shared__ int si[kCandMax];
-  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-  const int V = a.vocab;
-  // Buffer loads of the row (32-bit offsets; reads past it return 0).
-  const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.logits + (int64_t)row * V, (uint32_t)V * 2u);
-  const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.seen + (int64_t)row * a.seen_pitch, (uint32_t)V);
-
-  // Element j of this thread: token j * kCandThreads + tid; fp16 bits, two
-  // per register (past the vocabulary: -inf, never counted).
-  uint32_t xh[kCandPerThread / 2];
-  uint64_t seen_bits = 0;
+// Exclusive prefix sum over the threads of a T-thread workgroup (thread
+// order), and the total.
+template <int T>
+__device__ __forceinline__ uint32_t block_scan(uint32_t v, uint32_t* red, uint32_t* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t incl = v;
 #pragma unroll
-  for (int j = 0; j < kCandPerThread; j += 2) {
-    const uint32_t i0 = (uint32_t)(j * kCandThreads + tid), i1 = i0 + kCandThreads;
-    uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(lr, i0 * 2u, 0, 0);
-    uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(lr, i1 * 2u, 0, 0);
-    lo = i0 < (uint32_t)V ? lo : 0xfc00u;
-    hi = i1 < (uint32_t)V ? hi : 0xfc00u;
-    xh[j / 2] = lo | hi << 16;
-    seen_bits |= (uint64_t)(__builtin_amdgcn_raw_buffer_load_b8(sr, i0, 0, 0) != 0) << j;
-    seen_bits |= (uint64_t)(__builtin_amdgcn_raw_buffer_load_b8(sr, i1, 0, 0) != 0) << (j + 1);
-    if (j % 32 == 30) asm volatile("" ::: "memory");  // at most 64 loads in flight
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
   }
-  auto x_of = [&](int j) {
-    return half_bits_to_float((uint16_t)(j & 1 ? xh[j / 2] >> 16 : xh[j / 2] & 0xffffu));
-  };
-  float m = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < kCandPerThread; ++j) m = fmaxf(m, x_of(j));
-  m = block_reduce(m, true, red);
-  float sum = 0.f;
-#pragma unroll
-  for (int j = 0; j < kCandPerThread; ++j)
-    if (j * kCandThreads + tid < V) sum += expf(x_of(j) - m);
-  sum = block_reduce(sum, false, red);
-  const float lse = logf(sum);
-  // The penalized log-probability w of each element (v = w / temperature),
-  // held as its order-preserving key; 0 (below every finite value's key)
-  // past the vocabulary.
-  uint32_t kv[kCandPerThread];
-#pragma unroll
-  for (int j = 0; j < kCandPerThread; ++j) {
-    const float lp = (x_of(j) - m) - lse;
-    const float w = !(seen_bits >> j & 1u) ? lp : lp < 0.f ? lp * a.penalty : lp / a.penalty;
-    kv[j] = j * kCandThreads + tid < V ? order_key(w) : 0u;
+  __syncthreads();
+  if (lane == 63) red[w] = incl;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+  for (int i = 0; i < T / 64; ++i) {
+    before += i < w ? red[i] : 0u;
+    all += red[i];
   }
+  *total = all;
+  return before + incl - v;
+}
 
-  // Radix select of the kc-th largest w, 8 bits per pass from the top.
-  uint32_t prefix = 0, pmask = 0;
-  uint32_t need = (uint32_t)a.kc;
+// Key of the n-th largest flagged key of the workgroup (at least n flagged):
+// 8 bits per pass from the top, LDS histograms.
+template <int T, int J>
+__device__ uint32_t select_nth_key(const uint32_t (&key)[J], uint32_t flags, uint32_t n,
+                                   uint32_t* hist, uint32_t* pick) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  uint32_t prefix = 0, pmask = 0, need = n;
 #pragma unroll 1
   for (int shift = 24; shift >= 0; shift -= 8) {
-    if (tid < 256) hist[tid] = 0;
+    for (int b = tid; b < 256; b += T) hist[b] = 0;
     __syncthreads();
+    // Plain LDS atomics: they issue back to back (lanes on one address
+    // serialize in the LDS unit, not in the wave).
 #pragma unroll
-    for (int j = 0; j < kCandPerThread; ++j) {
-      const uint32_t key = kv[j];
-      const bool ok = key != 0u && (key & pmask) == prefix;
-      const uint32_t digit = (key >> shift) & 255u;
-      // Lanes that share a digit add once (up to 4 digits per wave; the
-      // rest add one each): few distinct digits mean many equal addresses.
-      uint64_t act = __ballot(ok);
-      for (int r = 0; r < 4 && act; ++r) {
-        const int leader = __ffsll((unsigned long long)act) - 1;
-        const uint32_t d0 = __shfl(digit, leader, 64);
-        const uint64_t same = __ballot((act >> lane & 1u) && digit == d0);
-        if (lane == leader) atomicAdd(&hist[d0], (uint32_t)__popcll(same));
-        act &= ~same;
-      }
-      if (act >> lane & 1u) atomicAdd(&hist[digit], 1u);
-    }
+    for (int j = 0; j < J; ++j)
+      if ((flags >> j & 1u) && (key[j] & pmask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
     __syncthreads();
     if (tid < 64) {
       // Lane L holds digits 255 - 4L .. 252 - 4L (the largest first).
@@ -317,35 +281,178 @@ __global__ __launch_bounds__(kCandThreads) void beam_candidates_kernel(BeamCandA
     prefix |= pick[0] << shift;
     pmask |= 255u << shift;
   }
-  const uint32_t kth = prefix;  // key of the kc-th largest w
+  return prefix;
+}
 
-  // Every entry with w >= the kc-th largest, as (v, token); then sorted: v
-  // descending, token ascending.
+struct CandLayout {  // the workspace of one call
+  float2* part;  // [beams][slices] (max, sum of exp)
+  int* count;    // [beams][slices][2] entries kept per class
+  float* x;      // [beams][slices][2][kc] logits
+  int* token;    // [beams][slices][2][kc]
+};
+__host__ __device__ inline CandLayout cand_layout(void* ws, int beams, int slices, int kc) {
+  char* p = static_cast<char*>(ws);
+  CandLayout l;
+  const int64_t parts = (int64_t)beams * slices;
+  l.part = reinterpret_cast<float2*>(p);
+  l.count = reinterpret_cast<int*>(p + parts * 8);
+  l.x = reinterpret_cast<float*>(p + parts * 16);
+  l.token = reinterpret_cast<int*>(p + parts * 16 + parts * 2 * kc * 4);
+  return l;
+}
+
+__global__ __launch_bounds__(kSliceThreads) void cand_slice_kernel(BeamCandArgs a) {
+  __shared__ float red[kSliceThreads / 64];
+  __shared__ uint32_t ured[kSliceThreads / 64];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t pick[2];
+  const int s = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  const int V = a.vocab, S = gridDim.x;
+  const CandLayout l = cand_layout(a.workspace, a.beams, S, a.kc);
+  const __amdgpu_buffer_rsrc_t lr = make_rsrc(a.logits + (int64_t)row * V, (uint32_t)V * 2u);
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.seen + (int64_t)row * a.seen_pitch, (uint32_t)V);
+  float x[kSliceJ];
+  uint32_t key[kSliceJ];
+  uint32_t valid = 0, seen = 0;
+#pragma unroll
+  for (int j = 0; j < kSliceJ; ++j) {
+    const uint32_t i = (uint32_t)(s * kSliceLen + j * kSliceThreads + tid);
+    const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(lr, i * 2u, 0, 0);
+    const uint32_t b = __builtin_amdgcn_raw_buffer_load_b8(sr, i, 0, 0);
+    const bool ok = i < (uint32_t)V;
+    x[j] = ok ? half_bits_to_float((uint16_t)h) : -INFINITY;
+    valid |= (uint32_t)ok << j;
+    seen |= (uint32_t)(ok && b != 0) << j;
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kSliceJ; ++j) m = fmaxf(m, x[j]);
+  m = block_reduce<kSliceThreads>(m, true, red);
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < kSliceJ; ++j)
+    if (valid >> j & 1u) sum += expf(x[j] - m);
+  sum = block_reduce<kSliceThreads>(sum, false, red);
+  if (tid == 0) l.part[row * S + s] = make_float2(m, sum);
+#pragma unroll
+  for (int j = 0; j < kSliceJ; ++j) key[j] = order_key(x[j]);
+
+  for (int c = 0; c < 2; ++c) {  // 0: unseen tokens, 1: seen
+    const uint32_t flags = valid & (c ? seen : ~seen);
+    uint32_t cnt;
+    block_scan<kSliceThreads>(__popc(flags), ured, &cnt);
+    const uint32_t n = min(cnt, (uint32_t)a.kc);
+    // The n-th largest key (every flagged key when there are at most kc).
+    const uint32_t kth = cnt > (uint32_t)a.kc
+                             ? select_nth_key<kSliceThreads, kSliceJ>(key, flags, n, hist, pick)
+                             : 0u;
+    uint32_t gt = 0, eq = 0;
+#pragma unroll
+    for (int j = 0; j < kSliceJ; ++j) {
+      gt += (flags >> j & 1u) && key[j] > kth;
+      eq += (flags >> j & 1u) && key[j] == kth;
+    }
+    uint32_t gtotal, etotal;
+    uint32_t gslot = block_scan<kSliceThreads>(gt, ured, &gtotal);
+    uint32_t eslot = gtotal + block_scan<kSliceThreads>(eq, ured, &etotal);
+    const int64_t base = ((int64_t)(row * S + s) * 2 + c) * a.kc;
+#pragma unroll
+    for (int j = 0; j < kSliceJ; ++j) {
+      if (!(flags >> j & 1u)) continue;
+      uint32_t slot;
+      if (key[j] > kth) slot = gslot++;
+      else if (key[j] == kth) slot = eslot++;
+      else continue;
+      if (slot < n) {
+        l.x[base + slot] = x[j];
+        l.token[base + slot] = s * kSliceLen + j * kSliceThreads + tid;
+      }
+    }
+    if (tid == 0) l.count[(row * S + s) * 2 + c] = (int)n;
+  }
+}
+
+__global__ __launch_bounds__(kCandThreads) void cand_merge_kernel(BeamCandArgs a, int S) {
+  __shared__ float red[kCandThreads / 64];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t pick[2];
+  __shared__ int count;
+  __shared__ float lv[kCandThreads * kMergeJ];
+  __shared__ int li[kCandThreads * kMergeJ];
+  __shared__ float sv[kCandMax];
+  __shared__ int si[kCandMax];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  __shared__ float row_lse[2];
+  __shared__ int counts[2 * kMaxSlices];
+  const CandLayout l = cand_layout(a.workspace, a.beams, S, a.kc);
+  // The row's max and log of the sum of exp(x - max), from the slices (wave
+  // 0, one slice per lane), and the slices' entry counts.
+  if (tid < 64) {
+    const float2 p = tid < S ? l.part[row * S + tid] : make_float2(-INFINITY, 0.f);
+    float m = p.x;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float sum = tid < S ? p.y * expf(p.x - m) : 0.f;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (tid == 0) {
+      row_lse[0] = m;
+      row_lse[1] = logf(sum);
+    }
+  } else if (tid < 64 + 2 * S) {
+    counts[tid - 64] = l.count[row * S * 2 + tid - 64];
+  }
+  __syncthreads();
+  const float m = row_lse[0], lse = row_lse[1];
+
+  // Entry e: slice e / (2 kc), class (e / kc) % 2, slot e % kc.
+  float v[kMergeJ];
+  int tok[kMergeJ];
+  uint32_t key[kMergeJ];
+  uint32_t flags = 0;
+#pragma unroll
+  for (int j = 0; j < kMergeJ; ++j) {
+    const int e = j * kCandThreads + tid;
+    const int s = e / (2 * a.kc), c = (e / a.kc) % 2, slot = e % a.kc;
+    const bool ok = s < S && slot < counts[s * 2 + c];
+    float w = -INFINITY;
+    tok[j] = 0;
+    if (ok) {
+      const int64_t at = ((int64_t)(row * S + s) * 2 + c) * a.kc + slot;
+      const float lp = (l.x[at] - m) - lse;
+      w = c == 0 ? lp : lp < 0.f ? lp * a.penalty : lp / a.penalty;
+      tok[j] = l.token[at];
+    }
+    key[j] = order_key(w);
+    v[j] = a.temperature != 1.0f ? w / a.temperature : w;
+    flags |= (uint32_t)ok << j;
+  }
+  const uint32_t kth = select_nth_key<kCandThreads, kMergeJ>(key, flags, (uint32_t)a.kc, hist, pick);
+
+  // Every entry with w >= the kc-th largest, sorted: v descending, token
+  // ascending.
   if (tid == 0) count = 0;
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < kCandPerThread; ++j) {
-    const int i = j * kCandThreads + tid;
-    const bool ok = kv[j] != 0u && kv[j] >= kth;
+  for (int j = 0; j < kMergeJ; ++j) {
+    const bool ok = (flags >> j & 1u) && key[j] >= kth;
     const uint64_t mask = __ballot(ok);
     if (mask) {
       const int leader = __ffsll((unsigned long long)mask) - 1;
       int base = 0;
       if (lane == leader) base = atomicAdd(&count, __popcll(mask));
-      base = __shfl(base, leader, 64);
+      base = __builtin_amdgcn_readlane(base, leader);
       const int slot = base + (int)__builtin_amdgcn_mbcnt_hi(
                                   (uint32_t)(mask >> 32),
                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-      if (ok && slot < kCandCap) {
-        const float w = key_value(kv[j]);
-        lv[slot] = a.temperature != 1.0f ? w / a.temperature : w;
-        li[slot] = i;
+      if (ok) {
+        lv[slot] = v[j];
+        li[slot] = tok[j];
       }
     }
   }
   __syncthreads();
-  const int total = count;
-  const int n = min(total, kCandCap);
+  const int n = count;
   for (int t = tid; t < n; t += kCandThreads) {
     const float x = lv[t];
     const int ix = li[t];
@@ -363,7 +470,7 @@ __global__ __launch_bounds__(kCandThreads) void beam_candidates_kernel(BeamCandA
     const bool in = d < a.kc;
     float x = in ? sv[d] : -INFINITY;
     const float thr = sv[a.k - 1];
-    const bool overflow = total > kCandCap || (a.kc < V && sv[a.kc - 1] == thr);
+    const bool overflow = a.kc < a.vocab && sv[a.kc - 1] == thr;
     if (x < thr) x = -INFINITY;
     if (a.use_top_p) {
       const float mx = sv[0];
@@ -390,14 +497,14 @@ __global__ __launch_bounds__(kCandThreads) void beam_candidates_kernel(BeamCandA
 }
 
 __global__ __launch_bounds__(kCandThreads) void beam_joint_kernel(BeamCandArgs a) {
-  __shared__ float red[kCandWaves];
+  __shared__ float red[kCandThreads / 64];
   __shared__ int nonzero;
   const int tid = threadIdx.x;
   const int n = a.beams * a.kc;
   const float s = tid < n ? a.scores[tid] : -INFINITY;
-  const float m = block_reduce(s, true, red);
+  const float m = block_reduce<kCandThreads>(s, true, red);
   const float e = s == -INFINITY ? 0.f : expf(s - m);
-  const float total = block_reduce(e, false, red);
+  const float total = block_reduce<kCandThreads>(e, false, red);
   const float p = e / total;
   if (tid == 0) nonzero = 0;
   __syncthreads();
@@ -415,9 +522,20 @@ __global__ __launch_bounds__(kCandThreads) void beam_joint_kernel(BeamCandArgs a
 
 }  // namespace
 
+int beam_candidate_slices(int vocab) { return (vocab + kSliceLen - 1) / kSliceLen; }
+
+int64_t beam_candidates_workspace(int beams, int vocab, int kc) {
+  const int64_t parts = (int64_t)beams * beam_candidate_slices(vocab);
+  return parts * 16 + parts * 2 * kc * 8;
+}
+
 hipError_t launch_beam_candidates(const BeamCandArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(beam_candidates_kernel, dim3(a.beams), dim3(kCandThreads), 0, stream, a);
+  const int S = beam_candidate_slices(a.vocab);
+  hipLaunchKernelGGL(cand_slice_kernel, dim3(S, a.beams), dim3(kSliceThreads), 0, stream, a);
   hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(cand_merge_kernel, dim3(a.beams), dim3(kCandThreads), 0, stream, a, S);
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(beam_joint_kernel, dim3(1), dim3(kCandThreads), 0, stream, a);
   return hipGetLastError();

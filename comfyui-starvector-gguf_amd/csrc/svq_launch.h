@@ -162,7 +162,9 @@ struct BeamCandArgs {
   float temperature;
   float top_p_cut;         // 1 - top_p
   int use_top_p;
+  void* workspace;         // beam_candidates_workspace bytes, 8-byte aligned
 };
+int64_t beam_candidates_workspace(int beams, int vocab, int kc);
 hipError_t launch_beam_candidates(const BeamCandArgs& a, hipStream_t stream);
 
 hipError_t launch_dequant(const uint8_t* q, const uint16_t* s, void* out,

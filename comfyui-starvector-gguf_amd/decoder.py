@@ -485,12 +485,13 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
         cand_scores = torch.empty((beams, kc), device=device)
         cand_probs = torch.empty(beams * kc, device=device)
         status = torch.empty(2 + beams, dtype=torch.long, device=device)
+        cand_ws = native.beam_candidates_workspace(beams, vocab, kc, device)
     for step in range(steps):
         seen_now, seen_next = seen_rows[step % 2], seen_rows[1 - step % 2]
         if fused:
             native.beam_candidates(logits.contiguous(), seen_now, running_t, k, kc, 2,
                                    REPETITION_PENALTY, temperature, top_p, cand, cand_scores,
-                                   cand_probs, status)
+                                   cand_probs, status, cand_ws)
             noise = torch.empty((1, beams * vocab), device=device).exponential_()
             possible, overflow = status[:2].tolist()
         else:

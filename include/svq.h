@@ -271,19 +271,26 @@ int svq_beam_select(const float *probs, const float *noise, const float *scores,
  *   scores      fp32 [beams, kc] out: warped log-prob + running (-inf if removed)
  *   probs       fp32 [beams * kc] out: joint softmax of scores
  *   status      int64 [2 + beams] out: number of non-zero probs; 1 if any row
- *               overflows (more than 1024 values tie with its kc-th largest, or
- *               its kc-th largest equals its k-th: the candidates may then miss
- *               tokens the reference keeps, and the caller must warp the whole
- *               vocabulary); then the flag per row
+ *               overflows (its kc-th largest value equals its k-th: the
+ *               candidates may then miss tokens the reference keeps, and the
+ *               caller must warp the whole vocabulary); then the flag per row
+ *   workspace   svq_beam_candidates_workspace(beams, vocab, kc) bytes, 8-byte
+ *               aligned, written and read within the call (no initialization)
  * beams <= 8, vocab <= 65536, 1 <= k <= kc <= min(64, vocab), keep <= kc.
  * Sums add in another order than torch's reductions: results agree with the
- * reference's to rounding. Asynchronous on `stream`; svq_beam_select with
- * compact = 1 draws from these outputs.
+ * reference's to rounding. Asynchronous on `stream` (three kernels); calls
+ * that share a workspace must not overlap. svq_beam_select with compact = 1
+ * draws from these outputs.
  */
 int svq_beam_candidates(const uint16_t *logits, const uint8_t *seen, int64_t seen_pitch,
                         const float *running, int beams, int vocab, int k, int kc, int keep,
                         float penalty, float temperature, double top_p, int64_t *candidates,
-                        float *scores, float *probs, int64_t *status, void *stream);
+                        float *scores, float *probs, int64_t *status, void *workspace,
+                        int64_t workspace_bytes, void *stream);
+
+/* Bytes of workspace svq_beam_candidates needs (a negative SVQ_E* code for
+ * an invalid shape). */
+int64_t svq_beam_candidates_workspace(int beams, int vocab, int kc);
 
 /*
  * GGUF container reader (host memory; no GPU needed). Replaces the PyPI

@@ -262,13 +262,13 @@ def test_beam_select_rejects_bad_arguments(kw, code):
 def beam_candidates(**kw):
     args = dict(logits=FAKE, seen=FAKE, pitch=320, running=FAKE, beams=2, vocab=320, k=50, kc=64,
                 keep=2, penalty=3.1, temperature=1.5, top_p=0.9, candidates=FAKE, scores=FAKE,
-                probs=FAKE, status=FAKE)
+                probs=FAKE, status=FAKE, workspace=FAKE, workspace_bytes=1 << 20)
     args.update(kw)
     return native.load().svq_beam_candidates(
         args["logits"], args["seen"], args["pitch"], args["running"], args["beams"],
         args["vocab"], args["k"], args["kc"], args["keep"], args["penalty"],
         args["temperature"], args["top_p"], args["candidates"], args["scores"], args["probs"],
-        args["status"], None)
+        args["status"], args["workspace"], args["workspace_bytes"], None)
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -277,8 +277,19 @@ def beam_candidates(**kw):
     (dict(keep=65), -2), (dict(keep=-1), -2), (dict(pitch=304), -2), (dict(pitch=328), -2),
     (dict(temperature=0.0), -2), (dict(penalty=-1.0), -2), (dict(top_p=1.5), -2),
     (dict(logits=None), -3), (dict(status=None), -3), (dict(logits=FAKE + 1), -6),
-    (dict(candidates=FAKE + 4), -6), (dict(status=FAKE + 4), -6),
+    (dict(candidates=FAKE + 4), -6), (dict(status=FAKE + 4), -6), (dict(workspace=None), -3),
+    (dict(workspace=FAKE + 4), -6), (dict(workspace_bytes=100), -7),
 ])
 def test_beam_candidates_rejects_bad_arguments(kw, code):
     assert beam_candidates(**kw) == code
     assert native.load().svq_last_error().decode()
+
+
+def test_beam_candidates_workspace_size():
+    lib = native.load()
+    # Per row and slice of 4096 tokens: (max, sum), two counts, and kc
+    # (logit, token) pairs per class.
+    assert lib.svq_beam_candidates_workspace(2, 49152, 64) == 2 * 12 * (16 + 2 * 64 * 8)
+    assert lib.svq_beam_candidates_workspace(1, 320, 64) == 16 + 2 * 64 * 8
+    assert lib.svq_beam_candidates_workspace(9, 320, 64) == -2
+    assert lib.svq_beam_candidates_workspace(2, 320, 65) == -2

@@ -176,8 +176,9 @@ def run_candidates(logits, seen, running, temperature, top_p, keep=2):
     scores = torch.full((beams, kc), 7.0, device=dev)
     probs = torch.full((beams * kc,), 7.0, device=dev)
     status = torch.full((2 + beams,), -7, dtype=torch.long, device=dev)
+    ws = native.beam_candidates_workspace(beams, vocab, kc, dev)
     native.beam_candidates(logits, seen, running, k, kc, keep, decoder.REPETITION_PENALTY,
-                           temperature, top_p, cand, scores, probs, status)
+                           temperature, top_p, cand, scores, probs, status, ws)
     torch.cuda.synchronize()
     return cand, scores, probs.view(beams, kc), status
 
