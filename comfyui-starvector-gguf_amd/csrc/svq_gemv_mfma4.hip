@@ -143,11 +143,6 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)n * row_bytes);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)n * (uint32_t)kb * 2u);
   const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bias, a.bias ? (uint32_t)n * 2u : 0u);
-  // The residual is read with the bias, a tile ahead (not for fp32 output
-  // or split-K partials, which take none).
-  const bool has_res = a.residual && !a.y_f32 && SL == 1;
-  const __amdgpu_buffer_rsrc_t rr =
-      make_rsrc(a.residual, has_res ? (uint32_t)M * (uint32_t)n * 2u : 0u);
 
   if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
   constexpr int XP = T::kUnitWeights / 8;  // 16-byte x pieces per unit
@@ -231,19 +226,13 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
     }
   };
 
-  auto load_bias = [&](int tile, uint32_t (&bb)[R], uint32_t (&rb)[R][M]) {
+  auto load_bias = [&](int tile, uint32_t (&bb)[R]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int row = tile * tile_rows + r * 4 + ri;
       const uint32_t oob = (uint32_t)(!(tile < tiles && row < n)) * kOutOfRange;
-      const uint32_t rc = (uint32_t)(row < n ? row : 0);
-      bb[r] = __builtin_amdgcn_raw_buffer_load_b16(br, rc * 2u + oob, 0, 0);
-      if (has_res) {
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-          rb[r][m] = __builtin_amdgcn_raw_buffer_load_b16(rr, ((uint32_t)m * n + rc) * 2u + oob,
-                                                          0, 0);
-      }
+      bb[r] = __builtin_amdgcn_raw_buffer_load_b16(br, (uint32_t)(row < n ? row : 0) * 2u + oob,
+                                                   0, 0);
     }
   };
 
@@ -255,8 +244,8 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   st.begin(lns);
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d);
-  uint32_t bias_bits[R], res_bits[R][M] = {};
-  load_bias(tile_of(0), bias_bits, res_bits);
+  uint32_t bias_bits[R];
+  load_bias(tile_of(0), bias_bits);
   st.finish(xs, sxs, lns);
 
   float acc[R][M];
@@ -356,7 +345,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                   const float v = __builtin_fmaf(acc[r][m], Mfma4Traits<QT>::kOutScale, b);
-                  store_y_loaded(a, (size_t)m * n + row, v, (uint16_t)res_bits[r][m]);
+                  store_y(a, m, row, v);
                 }
               }
             }
@@ -368,7 +357,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
           for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
         cit = st0;
         ++cj;
-        load_bias(tile_of(cj), bias_bits, res_bits);
+        load_bias(tile_of(cj), bias_bits);
       }
     }
   }

@@ -81,10 +81,6 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)n * row_bytes);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)n * (uint32_t)kb * 2u);
   const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bias, a.bias ? (uint32_t)n * 2u : 0u);
-  // The residual is read with the bias, a tile ahead (fp32 output takes none).
-  const bool has_res = a.residual && !a.y_f32;
-  const __amdgpu_buffer_rsrc_t rr =
-      make_rsrc(a.residual, has_res ? (uint32_t)M * (uint32_t)n * 2u : 0u);
 
   // Static LDS: the Q5_0 mask table (a compile-time address, so lookups
   // need no base register). Dynamic LDS: x pieces, then offset sums.
@@ -131,18 +127,12 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
     }
   };
 
-  auto load_bias = [&](int tile, uint32_t (&bb)[R], uint32_t (&rb)[R][M]) {
+  auto load_bias = [&](int tile, uint32_t (&bb)[R]) {
     const uint32_t oob = (uint32_t)(tile >= tiles) * kOutOfRange;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int row = min(tile * tile_rows + rg * R + r, n - 1);
       bb[r] = __builtin_amdgcn_raw_buffer_load_b16(br, (uint32_t)row * 2u + oob, 0, 0);
-      if (has_res) {
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-          rb[r][m] = __builtin_amdgcn_raw_buffer_load_b16(
-              rr, ((uint32_t)m * n + (uint32_t)row) * 2u + oob, 0, 0);
-      }
     }
   };
 
@@ -157,8 +147,8 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   st.begin(lns);
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d);
-  uint32_t bias_bits[R], res_bits[R][M] = {};
-  load_bias(wid, bias_bits, res_bits);
+  uint32_t bias_bits[R];
+  load_bias(wid, bias_bits);
   st.finish(xs, sxs, lns);
 
   float acc[R][M];
@@ -216,7 +206,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
 #pragma unroll
               for (int m = 0; m < M; ++m) {
                 const float v = __builtin_fmaf(acc[r][m], T::kOutScale, b);
-                store_y_loaded(a, (size_t)m * n + row, v, (uint16_t)res_bits[r][m]);
+                store_y(a, m, row, v);
               }
             }
           }
@@ -227,7 +217,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
           for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
         cit = 0;
         ++cj;
-        load_bias(wid + cj * W, bias_bits, res_bits);
+        load_bias(wid + cj * W, bias_bits);
       }
     }
   }
