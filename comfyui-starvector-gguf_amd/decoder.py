@@ -248,12 +248,17 @@ class Starcoder2Decoder(nn.Module):
         logits = self.lm_head(self.norm(x[:, -1]))
         return CachedDecoding(self, keys, values, length), logits.expand(rows, -1)
 
-    def decode(self, tokens, position, keys, values, span):
-        """One token per row at `position`, attending the first `span` slots."""
+    def decode(self, tokens, position, keys, values, span, rope=None):
+        """One token per row at `position`, attending the first `span` slots.
+        `rope`: (cos, sin) tables over all cache slots (`_rope` of every
+        position, computed once), or None to compute this position's."""
         slots = torch.arange(span, device=keys.device)
         hidden_slots = (slots > position) | (slots <= position - self.cfg.window)
         bias = torch.zeros(span, device=keys.device, dtype=keys.dtype).masked_fill_(hidden_slots, float("-inf"))
-        cos, sin = self._rope(position, keys.dtype)
+        if rope is None:
+            cos, sin = self._rope(position, keys.dtype)
+        else:  # the same elementwise values, gathered
+            cos, sin = rope[0].index_select(0, position), rope[1].index_select(0, position)
         x = self.embed_tokens(tokens)[:, None]
         for layer, lk, lv in zip(self.layers, keys, values):
             x = layer(x, cos, sin, lk[:, :, :span], lv[:, :, :span], position, bias)
@@ -272,6 +277,8 @@ class CachedDecoding:
         self.tokens = torch.zeros(keys.shape[1], dtype=torch.long, device=keys.device)
         self.position = torch.full((1,), length, dtype=torch.long, device=keys.device)
         self.graphs = {}
+        # RoPE angles of every cache slot, once (a decode step gathers its row).
+        self.rope = model._rope(torch.arange(keys.shape[3], device=keys.device), keys.dtype)
         if keys.is_cuda:
             # Allocated here, outside any capture, for the largest span; the
             # decode steps reuse it.
@@ -286,7 +293,8 @@ class CachedDecoding:
         return min(self.keys.shape[-2], max(512, 1 << self.length.bit_length()))
 
     def _decode(self, span):
-        return self.model.decode(self.tokens, self.position, self.keys, self.values, span)
+        return self.model.decode(self.tokens, self.position, self.keys, self.values, span,
+                                 self.rope)
 
     def step(self, tokens):
         """One decode step for `tokens` [rows] (None: already in self.tokens)."""

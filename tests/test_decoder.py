@@ -265,3 +265,22 @@ def test_stable_descending_is_python_sorted(values):
     want = sorted(range(len(values)), key=values.__getitem__, reverse=True)
     assert got_order.tolist() == want
     assert got_values.tolist() == [values[i] for i in want]
+
+
+def _rope_table_matches(device, dtype):
+    model = Starcoder2Decoder(SMALL, qtype="Q4_0", seed=3, device=device)
+    cos_t, sin_t = model._rope(torch.arange(600, device=device), dtype)
+    for p in (0, 1, 17, 511, 599):
+        cos, sin = model._rope(torch.tensor([p], device=device), dtype)
+        assert torch.equal(cos_t[p:p + 1], cos) and torch.equal(sin_t[p:p + 1], sin), p
+
+
+def test_rope_table_rows_equal_per_position_angles_cpu():
+    """A decode step gathers its RoPE row from a table of every slot: the rows
+    must be the per-position values bit for bit."""
+    _rope_table_matches("cpu", torch.float32)
+
+
+@pytest.mark.gpu
+def test_rope_table_rows_equal_per_position_angles_gpu(cuda_device):
+    _rope_table_matches(cuda_device, torch.float16)
