@@ -1,8 +1,9 @@
 // SoA dequantization for gfx950: every weight is the exact fp32 product of
 // its signed integer code and its block's fp16 scale, then rounded to the
 // output type, as `dequantize_soa` computes it (quantization.py:93-105).
-// One thread decodes one unit (16 or 20 payload bytes) and writes its 16 or
-// 32 outputs as contiguous 16-byte stores. The row-gather variant serves
+// One thread decodes a quarter block (8 weights) and writes them as one
+// 16-byte store (fp16 / bf16) or two (fp32), so a wave's stores are
+// contiguous. The row-gather variant (one thread per unit) serves
 // `GGUFEmbedding.forward` (quantization.py:421-446) without index_select
 // copies.
 #include "svq_device.h"
@@ -69,16 +70,58 @@ __device__ __forceinline__ void decode_unit(const uint8_t* q, const uint16_t* s,
   for (int j = 0; j < T::kUnitWeights; ++j) v[j] = (float)c[j] * d;
 }
 
+// Codes of weights 8p .. 8p + 7 of block b (piece p = 0..3 of its 32).
+// Q4_0 / Q5_0: weight j < 16 is the low nibble of payload byte j, weight
+// j >= 16 the high nibble of byte j - 16; Q5_0 adds bit j of its qh word as
+// bit 4. Q8_0: byte j as int8.
+template <int QT>
+__device__ __forceinline__ void decode_piece(const uint8_t* q, int64_t b, int p, int (&c)[8]) {
+  uint32_t lo, hi;
+  uint32_t qh = 0;
+  if constexpr (QT == 4) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(q + b * 16 + (p & 1) * 8);
+    lo = w[0];
+    hi = w[1];
+  } else if constexpr (QT == 5) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(q + b * 20);
+    qh = w[0];
+    lo = w[1 + (p & 1) * 2];
+    hi = w[2 + (p & 1) * 2];
+  } else {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(q + b * 32 + p * 8);
+    lo = w[0];
+    hi = w[1];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t byte = ((i < 4 ? lo : hi) >> (8 * (i & 3))) & 0xffu;
+    if constexpr (QT == 8) {
+      c[i] = (int)(int8_t)byte;
+    } else {
+      const int nib = (int)((byte >> ((p >> 1) * 4)) & 15u);
+      if constexpr (QT == 4) c[i] = nib - 8;
+      else c[i] = (nib | (int)((qh >> (8 * p + i)) & 1u) << 4) - 16;
+    }
+  }
+}
+
+// One thread per 8 weights (a quarter block): a wave's stores cover
+// contiguous output (1 KB at fp16).
 template <int QT, int OUT>
 __global__ __launch_bounds__(kDqThreads) void dequant_kernel(
     const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
-    void* __restrict__ out, int64_t nunits) {
-  using T = QTraits<QT>;
-  const int64_t unit = (int64_t)blockIdx.x * kDqThreads + threadIdx.x;
-  if (unit >= nunits) return;
-  float v[T::kUnitWeights];
-  decode_unit<QT>(q, s, unit, v);
-  store_values<OUT>(out, unit * T::kUnitWeights, v);
+    void* __restrict__ out, int64_t npieces) {
+  const int64_t t = (int64_t)blockIdx.x * kDqThreads + threadIdx.x;
+  if (t >= npieces) return;
+  const int64_t b = t >> 2;
+  const int p = (int)(t & 3);
+  int c[8];
+  decode_piece<QT>(q, b, p, c);
+  const float d = half_bits_to_float(s[b]);
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = (float)c[j] * d;
+  store_values<OUT>(out, t * 8, v);
 }
 
 template <int QT, int OUT>
@@ -105,10 +148,10 @@ __global__ __launch_bounds__(kDqThreads) void dequant_rows_kernel(
 template <int QT, int OUT>
 static hipError_t dq(const uint8_t* q, const uint16_t* s, void* out,
                      int64_t nblocks, hipStream_t stream) {
-  const int64_t nunits = nblocks * QTraits<QT>::kUnitsPerBlock;
-  const int64_t groups = (nunits + kDqThreads - 1) / kDqThreads;
+  const int64_t npieces = nblocks * 4;
+  const int64_t groups = (npieces + kDqThreads - 1) / kDqThreads;
   hipLaunchKernelGGL((dequant_kernel<QT, OUT>), dim3((unsigned)groups),
-                     dim3(kDqThreads), 0, stream, q, s, out, nunits);
+                     dim3(kDqThreads), 0, stream, q, s, out, npieces);
   return hipGetLastError();
 }
 
