@@ -161,6 +161,28 @@ def gemv_case(pool, dev, stream, qtype, n, k, m, bias, trials=5, replays=3):
             "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "bytes": nbytes}
 
 
+def dequant_case(pool, dev, stream, qtype, out_dtype, n=18432, k=4608, trials=5, replays=3):
+    """`svq_dequant` of an n x k matrix (quantization.py:93-105 on the GPU):
+    median µs per launch over rotating weight copies, algorithmic bytes
+    (payload + scales read, output written)."""
+    blocks = n * k // 32
+    out_bytes = torch.tensor([], dtype=out_dtype).element_size() * n * k
+    nbytes = blocks * BLOCK_BYTES[qtype] + out_bytes
+    count = copies_for(blocks * BLOCK_BYTES[qtype], pool.q.numel() // 2)
+    pool.reset()
+    cps = pool.copies(qtype, n, k, count)
+    out = torch.empty((n, k), dtype=out_dtype, device=dev)
+    calls = [(lambda q=q, s=s: native.dequant(q, s.view(torch.uint8), out, qtype)) for q, s in cps]
+    graph = capture(calls, stream)
+    time_graph(graph, stream, 1)
+    ms = [time_graph(graph, stream, replays) / count for _ in range(trials)]
+    us = statistics.median(ms) * 1e3
+    del graph
+    return {"qtype": qtype, "n": n, "k": k, "out": str(out_dtype).replace("torch.", ""),
+            "us": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), "bytes": nbytes}
+
+
 def sweep_cases():
     cases = [("cfg1", "Q8_0", 8192, 2048, 1, True)]
     for n, k in ((2304, 2048), (2048, 2048), (8192, 2048), (2048, 8192), (49152, 2048)):
@@ -615,6 +637,14 @@ def main():
             sweep.append(r)
             log(f"{cfg} {qtype} {n}x{k} M={m}: {r['us']:.2f} us {r['gbs']:.0f} GB/s ({r['frac']:.1%})")
 
+    dequant = []
+    if not args.quick:
+        for qtype in ("Q4_0", "Q5_0", "Q8_0"):
+            for out_dtype in (torch.float16, torch.float32):
+                r = dequant_case(pool, dev, stream, qtype, out_dtype)
+                dequant.append(r)
+                log(f"dequant {qtype} -> {r['out']}: {r['us']:.2f} us {r['gbs']:.0f} GB/s")
+
     cpu = None
     if not args.quick and not args.no_cpu:
         log("cpu baseline ...")
@@ -645,6 +675,7 @@ def main():
         "cpu_baseline": cpu,
         "decode": decode,
         "sweep": sweep,
+        "dequant": dequant,
     }
     print(json.dumps(result), flush=True)
 
