@@ -239,14 +239,15 @@ class Starcoder2Decoder(nn.Module):
         cfg = self.cfg
         length = embeddings.shape[1]
         shape = (cfg.layers, rows, cfg.kv_heads, capacity, cfg.head_dim)
-        keys = torch.zeros(shape, device=embeddings.device, dtype=embeddings.dtype)
-        values = torch.zeros_like(keys)
+        # Keys and values in one allocation, so a beam reorder is one launch.
+        kv = torch.zeros((2,) + shape, device=embeddings.device, dtype=embeddings.dtype)
+        keys, values = kv[0], kv[1]
         cos, sin = self._rope(torch.arange(length, device=embeddings.device), embeddings.dtype)
         x = embeddings
         for layer, lk, lv in zip(self.layers, keys, values):
             x = layer(x, cos, sin, lk, lv)
         logits = self.lm_head(self.norm(x[:, -1]))
-        return CachedDecoding(self, keys, values, length), logits.expand(rows, -1)
+        return CachedDecoding(self, keys, values, length, kv), logits.expand(rows, -1)
 
     def decode(self, tokens, position, keys, values, span, rope=None):
         """One token per row at `position`, attending the first `span` slots.
@@ -272,8 +273,11 @@ class CachedDecoding:
     (runtime_shared.py:345-394): one HIP graph per power-of-two span of at
     least 512 slots, captured after an eager warm-up on a side stream."""
 
-    def __init__(self, model, keys, values, length):
+    def __init__(self, model, keys, values, length, kv=None):
+        """`kv`: the [2, ...] tensor whose halves are `keys` and `values`, if
+        they share one allocation."""
         self.model, self.keys, self.values, self.length = model, keys, values, length
+        self.kv = kv
         self.tokens = torch.zeros(keys.shape[1], dtype=torch.long, device=keys.device)
         self.position = torch.full((1,), length, dtype=torch.long, device=keys.device)
         self.graphs = {}
@@ -342,11 +346,14 @@ class CachedDecoding:
 
     def reorder_rows(self, parents):
         """`reorder` with the parents as a device int64 tensor [rows]: on the
-        GPU one kernel per cache (svq_cache_reorder) moves the rows whose parent
-        differs, with no host round trip; on the host it reads the parents and
-        calls `reorder`."""
+        GPU one kernel (svq_cache_reorder; one per cache if keys and values
+        are separate allocations) moves the rows whose parent differs, with no
+        host round trip; on the host it reads the parents and calls
+        `reorder`."""
         if self.keys.is_cuda:
-            for cache in (self.keys, self.values):
+            caches = (self.keys, self.values) if self.kv is None else \
+                (self.kv.view(-1, *self.kv.shape[2:]),)  # both, as 2 x layers planes
+            for cache in caches:
                 native.cache_reorder(cache, parents, self.length)
         else:
             self.reorder(parents.tolist())
@@ -520,6 +527,8 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
             probs = scores.softmax(-1)
             possible = int(torch.count_nonzero(probs))
         draws = min(keep, possible)
+        if draws < 1:  # no possible continuation: torch.multinomial's own error, as the reference
+            torch.multinomial(cand_probs.view(1, -1) if fused and not overflow else probs, draws)
         parents, tokens = history[step, 0], history[step, 1]
         if on_gpu and not overflow and draws >= 1:
             if fused:
