@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libsvq.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 QTYPE_CODE = {"Q4_0": 4, "Q5_0": 5, "Q8_0": 8}
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
@@ -63,8 +63,9 @@ def load() -> ctypes.CDLL:
         lib.svq_dequant_rows.restype = i32
         lib.svq_decode_attention_workspace.argtypes = [i32, i32, i32, i32]
         lib.svq_decode_attention_workspace.restype = i64
-        lib.svq_decode_attention.argtypes = [vp, i64, vp, vp, vp, vp, i64, vp, vp, i32, vp,
-                                             i32, i32, i32, i32, ctypes.c_float, vp, i64, vp]
+        lib.svq_decode_attention.argtypes = [vp, i64, vp, vp, vp, vp, i64, vp, vp, i32, i32,
+                                             vp, i32, i32, i32, i32, ctypes.c_float, vp, i64,
+                                             vp]
         lib.svq_decode_attention.restype = i32
         lib.svq_gemv_split.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp,
                                        i64, vp]
@@ -301,11 +302,12 @@ def attention_workspace(device: torch.device, rows: int, heads: int, kv_heads: i
 def decode_attention(qkv: torch.Tensor, cos: torch.Tensor | None, sin: torch.Tensor | None,
                      keys: torch.Tensor, values: torch.Tensor, position: torch.Tensor,
                      bias: torch.Tensor | None, out: torch.Tensor, heads: int, kv_heads: int,
-                     scale: float, workspace: torch.Tensor) -> None:
+                     scale: float, workspace: torch.Tensor, window: int = 0) -> None:
     """One layer's decode attention (svq_decode_attention). qkv [rows, >= (heads +
     2 kv_heads) * 128] fp16 with unit stride in its last dim; keys/values the
     layer's cache or a slot-prefix view of it, [rows, kv_heads, span, 128];
-    position a device int64 scalar; out [rows, heads * 128]."""
+    position a device int64 scalar; out [rows, heads * 128]; window > 0 masks
+    the slots outside (position - window, position]."""
     lib = load()
     if keys.dim() != 4 or values.shape != keys.shape or values.stride() != keys.stride():
         raise ValueError("keys and values must be [rows, kv_heads, span, head_dim] views "
@@ -334,8 +336,9 @@ def decode_attention(qkv: torch.Tensor, cos: torch.Tensor | None, sin: torch.Ten
         rc = lib.svq_decode_attention(
             qkv.data_ptr(), qkv.stride(0), None if cos is None else cos.data_ptr(),
             None if sin is None else sin.data_ptr(), keys.data_ptr(), values.data_ptr(),
-            capacity, position.data_ptr(), None if bias is None else bias.data_ptr(), span,
-            out.data_ptr(), rows, heads, kv_heads, head_dim, scale, workspace.data_ptr(),
+            capacity, position.data_ptr(), None if bias is None else bias.data_ptr(),
+            int(window), span, out.data_ptr(), rows, heads, kv_heads, head_dim, scale,
+            workspace.data_ptr(),
             workspace.numel(), _stream(qkv.device))
     _check(lib, "svq_decode_attention", rc)
 

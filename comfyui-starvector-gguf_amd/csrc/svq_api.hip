@@ -604,7 +604,7 @@ int64_t svq_decode_attention_workspace(int rows, int heads, int kv_heads, int sp
 int svq_decode_attention(const uint16_t* qkv, int64_t qkv_stride, const uint16_t* cos,
                          const uint16_t* sin, uint16_t* keys, uint16_t* values,
                          int64_t capacity, const int64_t* position, const uint16_t* bias,
-                         int span, uint16_t* out, int rows, int heads, int kv_heads,
+                         int window, int span, uint16_t* out, int rows, int heads, int kv_heads,
                          int head_dim, float scale, void* workspace,
                          int64_t workspace_bytes, void* stream) {
   if (rows < 1 || kv_heads < 1 || heads < kv_heads || heads % kv_heads != 0 ||
@@ -641,6 +641,7 @@ int svq_decode_attention(const uint16_t* qkv, int64_t qkv_stride, const uint16_t
   a.capacity = capacity;
   a.position = position;
   a.bias = bias;
+  a.window = window > 0 ? window : 0;
   a.span = span;
   a.out = out;
   a.kv_heads = kv_heads;

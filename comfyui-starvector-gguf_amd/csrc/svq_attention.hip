@@ -176,16 +176,23 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(vslab, (uint32_t)a.span * kD * 2);
 
   // Bias of the lane's two key/value slots s0 + 16t + n (bkv) and of its
-  // eight score slots s0 + 16t + 4g + i (bsc); -inf past the span.
+  // eight score slots s0 + 16t + 4g + i (bsc); -inf past the span and, with
+  // a window, outside (position - window, position] (the decode step's
+  // causal sliding-window mask, runtime_8b.py:103-105).
+  auto hidden = [&](int j) { return a.window > 0 && (j > pos || j <= pos - a.window); };
   float bkv[2], bsc[2][4];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int j = s0 + 16 * t + n;
-    bkv[t] = j >= a.span ? -INFINITY : a.bias ? half_bits_to_float(a.bias[j]) : 0.0f;
+    bkv[t] = j >= a.span || hidden(j) ? -INFINITY
+             : a.bias               ? half_bits_to_float(a.bias[j])
+                                    : 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int js = s0 + 16 * t + 4 * g + i;
-      bsc[t][i] = js >= a.span ? -INFINITY : a.bias ? half_bits_to_float(a.bias[js]) : 0.0f;
+      bsc[t][i] = js >= a.span || hidden(js) ? -INFINITY
+                  : a.bias                   ? half_bits_to_float(a.bias[js])
+                                             : 0.0f;
     }
   }
 
@@ -198,7 +205,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_attention_kernel(AttnArgs 
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int j = s0 + 16 * t + n;
-    const bool load = j < a.span && j != pos && (a.bias == nullptr || j < pos);
+    const bool load = j < a.span && j != pos && !hidden(j) && (a.bias == nullptr || j < pos);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const uint32_t off = load ? (uint32_t)j * kD * 2 + (32u * ks + 8u * g) * 2 : kOutOfRange;

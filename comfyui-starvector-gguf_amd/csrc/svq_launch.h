@@ -87,6 +87,7 @@ struct AttnArgs {
   int64_t capacity;        // slots per (row, kv head) in the cache
   const int64_t* position; // device scalar: the slot of the new token
   const uint16_t* bias;    // fp16 [span] additive score bias, or nullptr
+  int window;              // > 0: slots j > position or j <= position - window masked
   int span;                // slots attended
   uint16_t* out;           // fp16 [rows, heads x 128]
   int kv_heads;

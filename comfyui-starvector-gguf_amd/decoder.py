@@ -121,7 +121,8 @@ class Starcoder2Block(nn.Module):
             out = torch.empty((rows, hidden), dtype=x.dtype, device=x.device)
             workspace = native.attention_workspace(x.device, rows, heads, kvh, keys.shape[2])
             native.decode_attention(qkv, cos.view(-1), sin.view(-1), keys, values, position,
-                                    bias, out, heads, kvh, hd ** -0.5, workspace)
+                                    bias, out, heads, kvh, hd ** -0.5, workspace,
+                                    window=cfg.window if bias is None else 0)
             x = fused_linear(self.o_proj, out, residual=x)
             h = fused_linear(self.c_fc, x, norm=self.post_attention_layernorm, gelu=True)
             split = native.split_workspace(x.device, rows, hidden, cfg.inner,
@@ -253,9 +254,13 @@ class Starcoder2Decoder(nn.Module):
         """One token per row at `position`, attending the first `span` slots.
         `rope`: (cos, sin) tables over all cache slots (`_rope` of every
         position, computed once), or None to compute this position's."""
-        slots = torch.arange(span, device=keys.device)
-        hidden_slots = (slots > position) | (slots <= position - self.cfg.window)
-        bias = torch.zeros(span, device=keys.device, dtype=keys.dtype).masked_fill_(hidden_slots, float("-inf"))
+        if keys.is_cuda:
+            bias = None  # the attention kernel masks from the position and the window
+        else:
+            slots = torch.arange(span, device=keys.device)
+            hidden_slots = (slots > position) | (slots <= position - self.cfg.window)
+            bias = torch.zeros(span, device=keys.device, dtype=keys.dtype).masked_fill_(
+                hidden_slots, float("-inf"))
         if rope is None:
             cos, sin = self._rope(position, keys.dtype)
         else:  # the same elementwise values, gathered

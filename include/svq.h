@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define SVQ_ABI_VERSION 1
+#define SVQ_ABI_VERSION 2
 
 /* Quantization codes: the reference's kernel codes (quantization.py:120). */
 #define SVQ_Q4_0 4
@@ -192,6 +192,9 @@ int64_t svq_decode_attention_workspace(int rows, int heads, int kv_heads, int sp
  *   position  device int64 scalar, 0 <= *position < span (a slot outside
  *             [0, span) is neither written nor attended)
  *   bias      fp16 [span] additive score bias (0 / -inf masks), or NULL
+ *   window    > 0: slots j > *position or j <= *position - window are masked
+ *             (-inf), the decode step's causal sliding window (runtime_8b.py:
+ *             103-105), in addition to `bias`; <= 0: no such mask
  *   out       fp16 [rows, heads x 128]
  * Query head h attends key/value head h / (heads / kv_heads). Scores are
  * rounded to fp16 as the reference's fp16 baddbmm stores them; softmax and
@@ -200,7 +203,7 @@ int64_t svq_decode_attention_workspace(int rows, int heads, int kv_heads, int sp
 int svq_decode_attention(const uint16_t *qkv, int64_t qkv_stride, const uint16_t *cos,
                          const uint16_t *sin, uint16_t *keys, uint16_t *values,
                          int64_t capacity, const int64_t *position, const uint16_t *bias,
-                         int span, uint16_t *out, int rows, int heads, int kv_heads,
+                         int window, int span, uint16_t *out, int rows, int heads, int kv_heads,
                          int head_dim, float scale, void *workspace,
                          int64_t workspace_bytes, void *stream);
 

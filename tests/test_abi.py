@@ -36,7 +36,7 @@ def test_library_exports_every_declared_function():
 
 
 def test_abi_version():
-    assert native.load().svq_abi_version() == native.ABI_VERSION == 1
+    assert native.load().svq_abi_version() == native.ABI_VERSION == 2
 
 
 FAKE = 1 << 20  # a 16-byte aligned non-null address; never dereferenced
@@ -119,9 +119,9 @@ def attention(**kw):
     lib = native.load()
     return lib.svq_decode_attention(
         args["qkv"], args["stride"], args["cos"], args["sin"], args["keys"], args["values"],
-        args["capacity"], args["position"], args["bias"], args["span"], args["out"],
-        args["rows"], args["heads"], args["kv_heads"], args["head_dim"], args["scale"],
-        args["workspace"], args["workspace_bytes"], None)
+        args["capacity"], args["position"], args["bias"], args.get("window", 0), args["span"],
+        args["out"], args["rows"], args["heads"], args["kv_heads"], args["head_dim"],
+        args["scale"], args["workspace"], args["workspace_bytes"], None)
 
 
 @pytest.mark.parametrize("kw,code", [

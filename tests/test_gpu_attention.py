@@ -89,7 +89,7 @@ def reference(case, round_probs=False):
     return keys, values, out
 
 
-def run_kernel(case, device, out=None, workspace=None):
+def run_kernel(case, device, out=None, workspace=None, window=0):
     dev = lambda t: None if t is None else t.to(device)
     keys, values = dev(case["keys"]), dev(case["values"])
     span = case["span"]
@@ -100,7 +100,7 @@ def run_kernel(case, device, out=None, workspace=None):
         device, rows, heads, kvh, span)
     native.decode_attention(dev(case["qkv"]), dev(case["cos"]), dev(case["sin"]),
                             keys[:, :, :span], values[:, :, :span], position, dev(case["bias"]),
-                            out, heads, kvh, HD ** -0.5, ws)
+                            out, heads, kvh, HD ** -0.5, ws, window=window)
     torch.cuda.synchronize()
     return keys.cpu(), values.cpu(), out.float().cpu()
 
@@ -133,6 +133,21 @@ CASES = [
     (2, 8, 2, 300, 290, 100, True, None, "zeros"),        # zero bias: slots past position attended
     (2, 36, 4, 600, 512, 450, True, 100, "causal"),       # window: masked slots before position
 ]
+
+
+@pytest.mark.parametrize("rows,heads,kvh,cap,span,pos,rope,window,bias",
+                         [c for c in CASES if c[-1] == "causal"])
+def test_decode_attention_window_mask_equals_bias(cuda_device, rows, heads, kvh, cap, span, pos,
+                                                   rope, window, bias):
+    """The kernel's own causal sliding-window mask (bias NULL, window w; the
+    decode step's form) gives what the explicit -inf bias gives, bit for bit."""
+    case = make_case(rows, heads, kvh, cap, span, pos, rope, window, bias)
+    w = window if window is not None else 1 << 20
+    keys, values, out = run_kernel(case, cuda_device)
+    masked = dict(case, bias=None)
+    mkeys, mvalues, mout = run_kernel(masked, cuda_device, window=w)
+    assert torch.equal(keys, mkeys) and torch.equal(values, mvalues)
+    assert torch.equal(out, mout)
 
 
 @pytest.mark.parametrize("rows,heads,kvh,cap,span,pos,rope,window,bias", CASES)
