@@ -213,7 +213,7 @@ bool choose_stream(int m, int n, int k, int qtype, const Tuning& tu, int* lg_out
 
 constexpr int kMfmaMinRows = 5;  // smallest M sent to the MFMA kernel by default
 
-// Streaming MFMA launch (M <= 4): row tiles of 4 rows (8 with two row sets
+// Streaming MFMA launch (M <= 8): row tiles of 4 rows (8 with two row sets
 // per lane) over 16 unit slots. Variant (the `rows` code): 3 = consecutive
 // units per lane (three Q4_0 / Q5_0 blocks, needs units % 48 == 0; one Q8_0
 // block), 2 = two row sets per lane, 1 = one. The 4 waves of a workgroup
@@ -224,7 +224,12 @@ constexpr int kMfmaMinRows = 5;  // smallest M sent to the MFMA kernel by defaul
 // number per CU, at most two (balanced_groups).
 bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_out,
                   int* ksplit_out, int* groups_out, int* wmax_out, size_t extra_lds = 0) {
-  if ((tu.path != 4 && tu.path != 0) || m > 4) return false;
+  if ((tu.path != 4 && tu.path != 0) || m > 8) return false;
+  // M = 5..8 runs two A halves per unpacked weight operand. Measured at the
+  // 8B shapes against the 16x16x32 kernel: faster at M = 5..7 on every shape
+  // (Q5_0 c_fc 39.1 -> 22.6 us, Q8_0 lm_head 94.8 -> 51.0 us at M = 5); at
+  // M = 8 as fast or faster for Q8_0 only (lm_head 75.8 -> 65.1 us).
+  if (tu.path == 0 && m == 8 && qtype != SVQ_Q8_0) return false;
   // Automatic choice (measured at the StarCoder2-8B and GPTBigCode-1B shapes):
   // the matrix-core path wins for Q5_0 at every M and for Q4_0 / Q8_0 from
   // M = 2; at M = 1 the vector path's dot products are cheap enough, except
@@ -247,7 +252,11 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   const int unit_run = qtype == SVQ_Q8_0 ? 2 : 3;
   // Defaults: variant 3 for Q5_0 and Q8_0 (measured 2-9% faster than two row
   // sets at K = 4608 and 18432); Q4_0 keeps two row sets, which share each x read.
-  int rows = tu.mfma_r ? tu.mfma_r : (qtype != SVQ_Q4_0 && multi ? 3 : 2);
+  // With two A halves (M >= 5) two row sets win for Q5_0 (c_fc 24.2 -> 22.6 us,
+  // lm_head 46.5 -> 40.2 us at M = 5) and for Q8_0 at M = 8 (lm_head 85.5 ->
+  // 65.1 us); Q8_0 keeps whole-block lanes at M = 5..7.
+  const bool rows3 = m <= 4 ? qtype != SVQ_Q4_0 : qtype == SVQ_Q8_0 && m < 8;
+  int rows = tu.mfma_r ? tu.mfma_r : (rows3 && multi ? 3 : 2);
   if (rows == 3 && !multi) rows = 2;
   int wmax = 0, tiles = 0;
   size_t lds = 0;
@@ -361,15 +370,17 @@ struct Fusion {
 };
 
 // K split across workgroups, for a caller that provides a workspace: rows
-// longer than 8192 weights at M = 2..4 without a LayerNorm are cut into SL
+// longer than 8192 weights at M = 2..8 without a LayerNorm are cut into SL
 // slices of at most 4608 weights (SL divides K / 32). Each workgroup stages
 // only its slice of x (18 KB at M = 2 instead of the whole row's 74 KB) and
 // writes raw partial sums; a second kernel adds the slices in order and
 // stores y. Measured on 4608 x 18432: M = 2 2.2-3.0 us faster (Q4_0 /
 // Q5_0), M = 4 7.5 us; at M = 1 the vector kernel's single pass is faster.
+// At M = 5..8 x of a long row does not fit in LDS at all (the chunked kernel,
+// 47-94 us on 4608 x 18432), so every slice runs the streaming MFMA kernel.
 // Returns SL, or 0 when the shape stays one pass.
 int split_slices(int m, int k, bool layer_norm) {
-  if (layer_norm || m < 2 || m > 4 || k <= 8192) return 0;
+  if (layer_norm || m < 2 || m > 8 || k <= 8192) return 0;
   const int kb = k / 32;
   for (int sl = 2; sl <= svq::kSplitMaxSlices; ++sl)
     if (kb % sl == 0 && k / sl <= 4608) return sl;
@@ -425,8 +436,10 @@ int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t
   // K split: each slice planned as a K / SL matrix of n * SL rows; the
   // workgroup count a multiple of SL (workgroup b takes slice b % SL).
   const int sl = workspace ? split_slices(m, k, f.layer_norm()) : 0;
+  Tuning tu_split = tu;  // slices always on the streaming MFMA kernel
+  if (tu_split.path == 0) tu_split.path = 4;
   if (sl && workspace_bytes >= split_workspace_bytes(m, n, k) &&
-      choose_mfma4(m, n * sl, k / sl, qtype, tu, &rows, &ksplit, &groups, &wmax)) {
+      choose_mfma4(m, n * sl, k / sl, qtype, tu_split, &rows, &ksplit, &groups, &wmax)) {
     a.ksplit = 1;
     a.slices = sl;
     a.partial = static_cast<float*>(workspace);

@@ -68,7 +68,7 @@ const void* mfma_kernel(int qtype, int m, int rows);
 hipError_t launch_gemv_mfma(const GemvArgs& a, int qtype, int m, int rows, int groups,
                             hipStream_t stream);
 
-// Streaming MFMA kernel (svq_gemv_mfma4.hip), 1 <= M <= 4: function pointer
+// Streaming MFMA kernel (svq_gemv_mfma4.hip), 1 <= M <= 8: function pointer
 // and launcher (LDS layout and size as the vector streaming kernel).
 const void* mfma4_kernel(int qtype, int m, int rows, bool ln = false);
 size_t mfma4_lds_bytes(int qtype, int m, int k, int rows, int ksplit);

@@ -116,7 +116,7 @@ int svq_gemv_fused(const void *x, const uint8_t *q, const uint16_t *s,
 
 /*
  * svq_gemv_fused without the LayerNorm, with a caller-provided workspace
- * that lets long rows (K > 8192 at m = 2..4) split K across workgroups: each
+ * that lets long rows (K > 8192 at m = 2..8) split K across workgroups: each
  * workgroup stages only a slice of x (at most 4608 columns) and writes fp32
  * partial sums to the workspace, and a second kernel adds the slices in a
  * fixed order and applies bias, activation and residual. Same results as

@@ -224,11 +224,14 @@ def test_gemv_split_workspace_size():
     lib = native.load()
     assert lib.svq_gemv_split_workspace(2, 4608, 18432, 5) == 4 * 2 * 4608 * 4
     assert lib.svq_gemv_split_workspace(1, 4608, 18432, 4) == 0   # m = 1: one pass
+    assert lib.svq_gemv_split_workspace(8, 4608, 18432, 4) == 4 * 8 * 4608 * 4
+    assert lib.svq_gemv_split_workspace(5, 100, 9216, 8) == 2 * 5 * 100 * 4
     assert lib.svq_gemv_split_workspace(4, 100, 9216, 8) == 2 * 4 * 100 * 4
     assert lib.svq_gemv_split_workspace(2, 100, 12288, 4) == 3 * 2 * 100 * 4
     assert lib.svq_gemv_split_workspace(2, 4608, 4608, 5) == 0   # one pass
     assert lib.svq_gemv_split_workspace(2, 2048, 8192, 4) == 0   # K <= 8192
-    assert lib.svq_gemv_split_workspace(5, 4608, 18432, 5) == 0  # m > 4
+    assert lib.svq_gemv_split_workspace(5, 4608, 18432, 5) == 4 * 5 * 4608 * 4
+    assert lib.svq_gemv_split_workspace(9, 4608, 18432, 5) < 0   # m > 8
     assert lib.svq_gemv_split_workspace(2, 64, 40, 4) == -2
     assert lib.svq_gemv_split_workspace(2, 64, 64, 3) == -1
 

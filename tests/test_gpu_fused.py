@@ -173,6 +173,11 @@ SPLIT_SHAPES = [
     (3, 77, 9216, "Q8_0"),     # two slices
     (2, 300, 12288, "Q5_0"),   # three slices
     (4, 64, 18432, "Q5_0"),
+    (8, 4608, 18432, "Q5_0"),  # 8B c_proj at beam 8: x rows 4..7 in the second A half
+    (8, 4608, 18432, "Q4_0"),
+    (5, 130, 18432, "Q8_0"),
+    (7, 77, 9216, "Q4_0"),
+    (6, 300, 12288, "Q8_0"),
 ]
 
 

@@ -220,7 +220,7 @@ def test_gemv_decoder_shapes(cuda_device, kernel_path, qtype, n, k, m, has_bias)
     say(f"gemv decoder shape {kernel_path} {qtype} m={m} n={n} k={k} bias={has_bias}")
     if kernel_path == "mfma":
         assert native.gemv_plan(m, n, k, qtype)["kernel"] == "mfma"
-    if kernel_path == "mfma4" and m <= 4:
+    if kernel_path == "mfma4" and stream_eligible(qtype, m, n, k):
         assert native.gemv_plan(m, n, k, qtype)["kernel"] == "mfma4"
     q, s = gpu_soa(qtype, n, k, seed=n + k + m, dev=cuda_device)
     g = torch.Generator(device=cuda_device).manual_seed(m)
@@ -298,14 +298,14 @@ def stream_eligible(qtype, m, n, k):
 @pytest.mark.parametrize("qtype", QTYPES)
 def test_gemv_every_kernel_against_oracle(cuda_device, kernel_path, qtype):
     rng = np.random.default_rng(7)
-    for m in (1, 2, 3, 4, 8):
+    for m in (1, 2, 3, 4, 5, 7, 8):
         for n, k in ((1, 32), (13, 128), (33, 192), (129, 2048), (515, 4608), (40, 18432)):
             say(f"gemv {kernel_path} {qtype} m={m} n={n} k={k}")
             plan = native.gemv_plan(m, n, k, qtype)
             if kernel_path == "mfma":
                 assert (plan["kernel"] == "mfma") == mfma_eligible(qtype, m, n, k), plan
             if kernel_path == "mfma4":
-                assert (plan["kernel"] == "mfma4") == (m <= 4 and stream_eligible(qtype, m, n, k)), plan
+                assert (plan["kernel"] == "mfma4") == stream_eligible(qtype, m, n, k), plan
             q, s = orc.synthetic_soa(qtype, n, k, seed=n + k + m)
             x = rng.standard_normal((m, k)).astype(np.float16)
             bias = rng.standard_normal(n).astype(np.float16)
@@ -375,9 +375,11 @@ def test_gemv_mfma4_row_sets(cuda_device, monkeypatch, rows):
     monkeypatch.setenv("SVQ_MFMA_R", str(rows))
     rng = np.random.default_rng(rows)
     for qtype in QTYPES:
-        shapes = ((1, 77, 320), (2, 130, 1056), (3, 3, 96), (4, 261, 2048))
+        shapes = ((1, 77, 320), (2, 130, 1056), (3, 3, 96), (4, 261, 2048), (5, 19, 1056),
+                  (6, 130, 320), (7, 261, 96), (8, 515, 2048))
         if rows == 3:
-            shapes = ((1, 77, 1536), (2, 130, 4608), (3, 3, 3072), (4, 261, 1536))
+            shapes = ((1, 77, 1536), (2, 130, 4608), (3, 3, 3072), (4, 261, 1536), (5, 19, 3072),
+                      (6, 130, 1536), (7, 261, 4608), (8, 515, 1536))
         for m, n, k in shapes:
             say(f"gemv mfma4 rows={rows} {qtype} m={m} n={n} k={k}")
             assert native.gemv_plan(m, n, k, qtype)["rows"] == rows
@@ -400,7 +402,7 @@ def test_gemv_mfma4_ksplit(cuda_device, monkeypatch, rows, ksplit):
     monkeypatch.setenv("SVQ_MFMA_S", str(ksplit))
     rng = np.random.default_rng(10 * rows + ksplit)
     for qtype in QTYPES:
-        for m, n, k in ((1, 37, 1536), (2, 130, 4608), (3, 9, 18432)):
+        for m, n, k in ((1, 37, 1536), (2, 130, 4608), (3, 9, 18432), (6, 21, 3072), (8, 130, 4608)):
             plan = native.gemv_plan(m, n, k, qtype)
             say(f"gemv mfma4 rows={rows} ksplit={ksplit} {qtype} m={m} n={n} k={k} plan={plan}")
             assert plan["kernel"] == "mfma4" and plan["lg_g"] in (1, ksplit), plan
