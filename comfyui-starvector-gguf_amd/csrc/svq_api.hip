@@ -49,14 +49,16 @@ bool aligned(const void* p, uintptr_t a) {
 // chunked kernels, SVQ_LDS_KB (LDS budget of the chunked kernel), and
 // SVQ_MFMA_R (MFMA row tiles per wave, 1 or 2; for the streaming MFMA kernel
 // 3 selects its three-units-per-lane Q5_0 variant), SVQ_MFMA_S (K splits, 1..16) and
-// SVQ_MFMA_P (tile slots per workgroup) of the MFMA kernel. Read on every
-// call, so a process may change them.
+// SVQ_MFMA_P (tile slots per workgroup) of the MFMA kernel, SVQ_GROUPS_PER_CU
+// (1 or 2: the most workgroups per CU of the streaming MFMA kernel). Read on
+// every call, so a process may change them.
 struct Tuning {
   int lg_g = -1;
   int rows = 0;
   int path = 0;  // 0 automatic, 1 streaming, 2 chunked, 3 mfma, 4 streaming mfma
   int lds_kb = 40;
   int mfma_r = 0, mfma_s = 0, mfma_p = 0;
+  int groups_per_cu = 0;  // streaming MFMA kernel: workgroups per CU (1 or 2), 0 automatic
 };
 
 Tuning tuning() {
@@ -73,12 +75,14 @@ Tuning tuning() {
   if (const char* v = getenv("SVQ_MFMA_R")) t.mfma_r = atoi(v);
   if (const char* v = getenv("SVQ_MFMA_S")) t.mfma_s = atoi(v);
   if (const char* v = getenv("SVQ_MFMA_P")) t.mfma_p = atoi(v);
+  if (const char* v = getenv("SVQ_GROUPS_PER_CU")) t.groups_per_cu = atoi(v);
   if (t.lg_g > 6) t.lg_g = 6;
   if (t.rows != 0 && t.rows != 1 && t.rows != 2) t.rows = 0;
   if (t.lds_kb < 4 || t.lds_kb > 64) t.lds_kb = 40;
   if (t.mfma_r < 1 || t.mfma_r > 3) t.mfma_r = 0;
   if (t.mfma_s < 0 || t.mfma_s > 16) t.mfma_s = 0;
   if (t.mfma_p < 0 || t.mfma_p > 16) t.mfma_p = 0;
+  if (t.groups_per_cu != 1 && t.groups_per_cu != 2) t.groups_per_cu = 0;
   return t;
 }
 
@@ -226,10 +230,12 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
                   int* ksplit_out, int* groups_out, int* wmax_out, size_t extra_lds = 0) {
   if ((tu.path != 4 && tu.path != 0) || m > 8) return false;
   // M = 5..8 runs two A halves per unpacked weight operand. Measured at the
-  // 8B shapes against the 16x16x32 kernel: faster at M = 5..7 on every shape
-  // (Q5_0 c_fc 39.1 -> 22.6 us, Q8_0 lm_head 94.8 -> 51.0 us at M = 5); at
-  // M = 8 as fast or faster for Q8_0 only (lm_head 75.8 -> 65.1 us).
-  if (tu.path == 0 && m == 8 && qtype != SVQ_Q8_0) return false;
+  // 8B shapes against the 16x16x32 kernel: faster for Q5_0 and Q8_0 at every
+  // M (Q5_0 c_fc 39.1 -> 22.6 us, Q8_0 lm_head 94.8 -> 51.0 us at M = 5; at M
+  // = 8 Q5_0 c_fc 31.0 -> 26.6 us, lm_head 52.1 -> 45.3 us, Q8_0 lm_head 75.8
+  // -> 65.1 us) and for Q4_0 at M = 5..6; Q4_0 at M = 7..8 is 1-2 us faster
+  // on the 16x16x32 kernel (lm_head 39.9 against 43.6 us at M = 8).
+  if (tu.path == 0 && m >= 7 && qtype == SVQ_Q4_0) return false;
   // Automatic choice (measured at the StarCoder2-8B and GPTBigCode-1B shapes):
   // the matrix-core path wins for Q5_0 at every M and for Q4_0 / Q8_0 from
   // M = 2; at M = 1 the vector path's dot products are cheap enough, except
@@ -261,7 +267,10 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   int wmax = 0, tiles = 0;
   size_t lds = 0;
   for (;;) {
-    lds = svq::mfma4_lds_bytes(qtype, m, k, rows, 4) + extra_lds;
+    // Occupancy of the launch without split K (no LDS for partial sums): at
+    // M = 8 (Q5_0, K = 4608) those 2 KB decide between one and two workgroups
+    // per CU (c_fc 31.2 -> 26.6 us).
+    lds = svq::mfma4_lds_bytes(qtype, m, k, rows, 1) + extra_lds;
     if (lds > kStreamLdsMax) return false;
     wmax = cus * waves_per_cu(dev, svq::mfma4_kernel(qtype, m, rows, extra_lds > 0), wpg, lds);
     const int tile_rows = rows == 2 ? 8 : 4;
@@ -288,9 +297,18 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
     ksplit = 2;
   }
   if (ksplit > steps) ksplit = 1;  // every wave needs at least one step
+  if (ksplit > 1) {  // the partial sums' LDS: occupancy again, or no split
+    const size_t lds_split = svq::mfma4_lds_bytes(qtype, m, k, rows, ksplit) + extra_lds;
+    if (lds_split > kStreamLdsMax)
+      ksplit = 1;
+    else
+      wmax = cus * waves_per_cu(dev, svq::mfma4_kernel(qtype, m, rows, extra_lds > 0), wpg,
+                                lds_split);
+  }
   const int slots = wpg / ksplit;
   const int tile_groups = (tiles + slots - 1) / slots;
-  const int cap = wmax / wpg;
+  int cap = wmax / wpg;
+  if (tu.groups_per_cu && cap > tu.groups_per_cu * cus) cap = tu.groups_per_cu * cus;
   int groups = tile_groups < cap ? tile_groups : cap;
   const int rounds = (tile_groups + groups - 1) / groups;
   groups = (tile_groups + rounds - 1) / rounds;
