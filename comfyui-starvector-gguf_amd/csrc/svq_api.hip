@@ -50,8 +50,9 @@ bool aligned(const void* p, uintptr_t a) {
 // SVQ_MFMA_R (MFMA row tiles per wave, 1 or 2; for the streaming MFMA kernel
 // 3 selects its three-units-per-lane Q5_0 variant), SVQ_MFMA_S (K splits, 1..16) and
 // SVQ_MFMA_P (tile slots per workgroup) of the MFMA kernel, SVQ_GROUPS_PER_CU
-// (1 or 2: the most workgroups per CU of the streaming MFMA kernel). Read on
-// every call, so a process may change them.
+// (1 or 2: the most workgroups per CU of the streaming MFMA kernel) and
+// SVQ_GROUPS (its exact workgroup count). Read on every call, so a process may
+// change them.
 struct Tuning {
   int lg_g = -1;
   int rows = 0;
@@ -59,6 +60,7 @@ struct Tuning {
   int lds_kb = 40;
   int mfma_r = 0, mfma_s = 0, mfma_p = 0;
   int groups_per_cu = 0;  // streaming MFMA kernel: workgroups per CU (1 or 2), 0 automatic
+  int groups = 0;         // streaming MFMA kernel: workgroup count, 0 automatic
 };
 
 Tuning tuning() {
@@ -76,6 +78,7 @@ Tuning tuning() {
   if (const char* v = getenv("SVQ_MFMA_S")) t.mfma_s = atoi(v);
   if (const char* v = getenv("SVQ_MFMA_P")) t.mfma_p = atoi(v);
   if (const char* v = getenv("SVQ_GROUPS_PER_CU")) t.groups_per_cu = atoi(v);
+  if (const char* v = getenv("SVQ_GROUPS")) t.groups = atoi(v);
   if (t.lg_g > 6) t.lg_g = 6;
   if (t.rows != 0 && t.rows != 1 && t.rows != 2) t.rows = 0;
   if (t.lds_kb < 4 || t.lds_kb > 64) t.lds_kb = 40;
@@ -83,6 +86,7 @@ Tuning tuning() {
   if (t.mfma_s < 0 || t.mfma_s > 16) t.mfma_s = 0;
   if (t.mfma_p < 0 || t.mfma_p > 16) t.mfma_p = 0;
   if (t.groups_per_cu != 1 && t.groups_per_cu != 2) t.groups_per_cu = 0;
+  if (t.groups < 0 || t.groups > (1 << 16)) t.groups = 0;
   return t;
 }
 
@@ -257,11 +261,15 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   const bool multi = qtype == SVQ_Q8_0 || units % 48 == 0;
   const int unit_run = qtype == SVQ_Q8_0 ? 2 : 3;
   // Defaults: variant 3 for Q5_0 and Q8_0 (measured 2-9% faster than two row
-  // sets at K = 4608 and 18432); Q4_0 keeps two row sets, which share each x read.
-  // With two A halves (M >= 5) two row sets win for Q5_0 (c_fc 24.2 -> 22.6 us,
-  // lm_head 46.5 -> 40.2 us at M = 5) and for Q8_0 at M = 8 (lm_head 85.5 ->
-  // 65.1 us); Q8_0 keeps whole-block lanes at M = 5..7.
-  const bool rows3 = m <= 4 ? qtype != SVQ_Q4_0 : qtype == SVQ_Q8_0 && m < 8;
+  // sets at K = 4608 and 18432). Q4_0 takes it from M = 2 (8B beam-2 decode
+  // 468 -> 479 steps/s; at M = 3..4 c_fc 16.1 -> 14.6 us and c_proj's slices
+  // 18.1 -> 16.9 us), except matrices over 64 MiB at M = 3..4 (lm_head 27.7
+  // against 28.5 us), and keeps two row sets, which share each x read, at M =
+  // 1. With two A halves (M >= 5) two row sets win for Q5_0 (c_fc 24.2 ->
+  // 22.6 us, lm_head 46.5 -> 40.2 us at M = 5) and for Q8_0 at M = 8
+  // (lm_head 85.5 -> 65.1 us); Q8_0 keeps whole-block lanes at M = 5..7.
+  const bool q4_rows3 = m == 2 || (m >= 3 && q_bytes <= (64ull << 20));
+  const bool rows3 = m <= 4 ? qtype != SVQ_Q4_0 || q4_rows3 : qtype == SVQ_Q8_0 && m < 8;
   int rows = tu.mfma_r ? tu.mfma_r : (rows3 && multi ? 3 : 2);
   if (rows == 3 && !multi) rows = 2;
   int wmax = 0, tiles = 0;
@@ -319,6 +327,7 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   // on the 8B c_fc and lm_head shapes at M = 1..4), and rounding short
   // matrices up to whole CUs 3-12% on qkv and o_proj.
   if (ksplit == 1) groups = balanced_groups(tile_groups, cus, cap);
+  if (tu.groups) groups = std::min(tu.groups, std::min(tile_groups, cap));
   *rows_out = rows;
   *ksplit_out = ksplit;
   *groups_out = groups;
