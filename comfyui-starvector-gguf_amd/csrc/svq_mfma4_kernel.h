@@ -63,11 +63,12 @@ template <> struct Mfma4Traits<8> {
   static constexpr float kOutScale = 0x1p24f;
 };
 
-// x pieces per thread loaded before the weight prologue (as the vector
-// streaming kernel): all of x for K = 4608 at M <= 2 with 256 threads.
+// x pieces per thread loaded before the weight prologue: all of x for K =
+// 4608 at M <= 4 with 256 threads, so x arrives in one load round trip (at M
+// = 3..4 batches of 4 took three in a row).
 template <int QT, int M>
 constexpr int kStage4Batch =
-    M <= 2 ? M * 144 * (QTraits<QT>::kUnitWeights / 8) * QTraits<QT>::kUnitsPerBlock / 256 + 1
+    M <= 4 ? M * 144 * (QTraits<QT>::kUnitWeights / 8) * QTraits<QT>::kUnitsPerBlock / 256 + 1
            : 4;
 
 // Sum of v over the 16 lanes b * 4 + i (b = 0..15) of each i: DPP rotations
