@@ -65,11 +65,13 @@ template <> struct Mfma4Traits<8> {
 
 // x pieces per thread loaded before the weight prologue: all of x for K =
 // 4608 at M <= 4 with 256 threads, so x arrives in one load round trip (at M
-// = 3..4 batches of 4 took three in a row).
+// = 3..4 batches of 4 took three in a row); 10 at M = 8 (two round trips for
+// K = 4608 instead of five: 0.3-1.0 us faster on the 8B shapes); 4 at M =
+// 5..7, where 10 measured up to 1.5 us slower.
 template <int QT, int M>
 constexpr int kStage4Batch =
     M <= 4 ? M * 144 * (QTraits<QT>::kUnitWeights / 8) * QTraits<QT>::kUnitsPerBlock / 256 + 1
-           : 4;
+           : M == 8 ? 10 : 4;
 
 // Sum of v over the 16 lanes b * 4 + i (b = 0..15) of each i: DPP rotations
 // by 4 and 8 inside each 16-lane row, then the gfx950 lane swaps across rows.
