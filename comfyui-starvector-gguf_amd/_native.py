@@ -15,10 +15,10 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libsvq.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 QTYPE_CODE = {"Q4_0": 4, "Q5_0": 5, "Q8_0": 8}
-DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+DTYPE_CODE = {torch.float16: 0, torch.float32: 1, torch.bfloat16: 2}
 
 _lib = None
 _lock = threading.Lock()
@@ -180,6 +180,19 @@ def _split(lib, x, q, s, y, qtype, bias, residual, activation, workspace) -> Non
 
 
 _split_workspaces: dict = {}
+# Workspaces replaced by larger ones. They stay allocated until the process
+# ends: a graph captured earlier keeps their addresses in its kernel nodes.
+_retired_workspaces: list = []
+
+
+def gemv_workspace_bytes(m: int, n: int, k: int, qtype: str) -> int:
+    """Bytes of workspace svq_gemv_split uses for this shape: the partial sums
+    when long rows split K across workgroups, 0 when the shape runs in one
+    pass."""
+    lib = load()
+    need = lib.svq_gemv_split_workspace(m, n, k, QTYPE_CODE[qtype])
+    _check(lib, "svq_gemv_split_workspace", min(need, 0))
+    return need
 
 
 def split_workspace(device: torch.device, m: int, n: int, k: int, qtype: str,
@@ -188,13 +201,12 @@ def split_workspace(device: torch.device, m: int, n: int, k: int, qtype: str,
     stream) -- per device with per_stream False, for callers that keep all
     their launches on one stream -- and grown as needed; None when the shape
     runs in one pass, or when the workspace would have to grow while the
-    stream is being captured into a graph or `allocate` is False. Calls that
-    share it are ordered by their stream."""
+    stream is being captured into a graph or `allocate` is False (the call
+    then runs in one pass). Calls that share it are ordered by their stream. A workspace that is replaced by a larger one
+    is kept allocated, since graphs captured with it still use it."""
     if device.type != "cuda":
         return None
-    lib = load()
-    need = lib.svq_gemv_split_workspace(m, n, k, QTYPE_CODE[qtype])
-    _check(lib, "svq_gemv_split_workspace", min(need, 0))
+    need = gemv_workspace_bytes(m, n, k, qtype)
     if need == 0:
         return None
     index = device.index if device.index is not None else torch.cuda.current_device()
@@ -203,6 +215,8 @@ def split_workspace(device: torch.device, m: int, n: int, k: int, qtype: str,
     if ws is None or ws.numel() < need:
         if not allocate or torch.cuda.is_current_stream_capturing():
             return None
+        if ws is not None:
+            _retired_workspaces.append(ws)
         ws = torch.empty(need, dtype=torch.uint8, device=torch.device("cuda", index))
         _split_workspaces[key] = ws
     return ws
@@ -284,16 +298,25 @@ def dequant_rows(q: torch.Tensor, s: torch.Tensor, ids: torch.Tensor, nrows: int
 _workspaces: dict = {}
 
 
-def attention_workspace(device: torch.device, rows: int, heads: int, kv_heads: int,
-                        span: int) -> torch.Tensor:
-    """A workspace for svq_decode_attention, cached per device and grown as
-    needed. Calls that share it must be ordered (one stream)."""
+def attention_workspace_bytes(rows: int, heads: int, kv_heads: int, span: int) -> int:
+    """Bytes of workspace svq_decode_attention needs for this shape."""
     lib = load()
     need = lib.svq_decode_attention_workspace(rows, heads, kv_heads, span)
     _check(lib, "svq_decode_attention_workspace", min(need, 0))
+    return need
+
+
+def attention_workspace(device: torch.device, rows: int, heads: int, kv_heads: int,
+                        span: int) -> torch.Tensor:
+    """A workspace for svq_decode_attention, cached per device and grown as
+    needed; a replaced one stays allocated (graphs captured with it still use
+    it). Calls that share it must be ordered (one stream)."""
+    need = attention_workspace_bytes(rows, heads, kv_heads, span)
     key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < need:
+        if ws is not None:
+            _retired_workspaces.append(ws)
         ws = torch.empty(need, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws

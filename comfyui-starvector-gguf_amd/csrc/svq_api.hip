@@ -43,6 +43,17 @@ bool aligned(const void* p, uintptr_t a) {
   return ((uintptr_t)p & (a - 1)) == 0;
 }
 
+static_assert(SVQ_F16 == svq::kOutF16 && SVQ_F32 == svq::kOutF32 && SVQ_BF16 == svq::kOutBF16,
+              "the dequantize kernels take the ABI's element type codes");
+
+// Whether the byte ranges [a, a + na) and [b, b + nb) share a byte (an
+// absent array, NULL, overlaps nothing).
+bool overlaps(const void* a, uint64_t na, const void* b, uint64_t nb) {
+  if (!a || !b || !na || !nb) return false;
+  const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
+  return pa < pb + nb && pb < pa + na;
+}
+
 // Launch-shape overrides for tuning sweeps and for tests that exercise every
 // kernel: SVQ_PATH ("mfma4", "mfma", "stream" or "chunked"), SVQ_LG_G (log2 lanes per
 // row, 0..6) and SVQ_ROWS (rows per lane group, 1 or 2) of the streaming and
@@ -431,7 +442,7 @@ int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t
     return fail(SVQ_E_RANGE, "n=%d k=%d exceeds the supported range", n, k);
   if (!x || !q || !s || !y) return fail(SVQ_E_NULL, "NULL x, q, s or y");
   if (y_dtype != SVQ_F16 && y_dtype != SVQ_F32)
-    return fail(SVQ_E_DTYPE, "y_dtype %d is not SVQ_F16 or SVQ_F32", y_dtype);
+    return fail(SVQ_E_DTYPE, "y_is_fp32 %d is not 0 (fp16) or 1 (fp32)", y_dtype);
   if (!aligned(x, 16) || !aligned(q, qtype == SVQ_Q5_0 ? 4 : 16) ||
       !aligned(s, 2) || (bias && !aligned(bias, 2)) ||
       !aligned(y, y_dtype == SVQ_F32 ? 4 : 2))
@@ -440,6 +451,36 @@ int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t
   // the offset the kernels use for loads that must not touch memory.
   if ((uint64_t)(k / 32) * payload_bytes(qtype) * 128 >= (1ull << 31))
     return fail(SVQ_E_RANGE, "row of %d weights too long", k);
+  // y is written while other workgroups still read the inputs (each stages
+  // all of x, the LayerNorm parameters, its weight rows, bias and residual),
+  // so y may share no byte with any of them; the residual may be y itself
+  // (each element is read, then written, by one thread). The workspace is
+  // written too.
+  {
+    const uint64_t y_bytes = (uint64_t)m * n * (y_dtype == SVQ_F32 ? 4 : 2);
+    const uint64_t blocks = (uint64_t)n * (k / 32);
+    const struct {
+      const void* p;
+      uint64_t bytes;
+    } inputs[] = {{x, (uint64_t)m * k * 2},
+                  {q, blocks * payload_bytes(qtype)},
+                  {s, blocks * 2},
+                  {bias, (uint64_t)n * 2},
+                  {f.ln_w, (uint64_t)k * 2},
+                  {f.ln_b, (uint64_t)k * 2},
+                  {f.residual != y ? f.residual : nullptr, (uint64_t)m * n * 2}};
+    for (const auto& in : inputs)
+      if (overlaps(y, y_bytes, in.p, in.bytes))
+        return fail(SVQ_E_SHAPE, "y overlaps an input (x, weights, bias, LayerNorm or residual)");
+    if (workspace && workspace_bytes > 0) {
+      if (overlaps(workspace, (uint64_t)workspace_bytes, y, y_bytes) ||
+          overlaps(workspace, (uint64_t)workspace_bytes, f.residual, (uint64_t)m * n * 2))
+        return fail(SVQ_E_SHAPE, "workspace overlaps y or the residual");
+      for (const auto& in : inputs)
+        if (overlaps(workspace, (uint64_t)workspace_bytes, in.p, in.bytes))
+          return fail(SVQ_E_SHAPE, "workspace overlaps an input");
+    }
+  }
   const Tuning tu = tuning();
   svq::GemvArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -513,8 +554,9 @@ const char* svq_last_error(void) { return g_error; }
 
 int svq_gemv(const void* x, const uint8_t* q, const uint16_t* s,
              const uint16_t* bias, void* y, int m, int n, int k, int qtype,
-             int y_dtype, void* stream) {
-  return gemv_impl(x, q, s, bias, y, m, n, k, qtype, y_dtype, Fusion{}, stream);
+             int y_is_fp32, void* stream) {
+  // y_is_fp32 is 0 (SVQ_F16) or 1 (SVQ_F32); anything else is rejected.
+  return gemv_impl(x, q, s, bias, y, m, n, k, qtype, y_is_fp32, Fusion{}, stream);
 }
 
 int64_t svq_gemv_split_workspace(int m, int n, int k, int qtype) {
@@ -531,7 +573,6 @@ int svq_gemv_split(const void* x, const uint8_t* q, const uint16_t* s, const uin
     return fail(SVQ_E_DTYPE, "unsupported activation %d", activation);
   if ((residual && !aligned(residual, 2)) || (workspace && !aligned(workspace, 16)))
     return fail(SVQ_E_ALIGN, "misaligned residual or workspace");
-  if (residual && residual != y && x == y) return fail(SVQ_E_SHAPE, "y must not alias x");
   if (workspace_bytes < 0) return fail(SVQ_E_WORKSPACE, "negative workspace size");
   Fusion f;
   f.residual = residual;
@@ -551,8 +592,6 @@ int svq_gemv_fused(const void* x, const uint8_t* q, const uint16_t* s, const uin
     return fail(SVQ_E_ALIGN, "misaligned LayerNorm parameters or residual");
   if ((ln_weight || ln_bias) && !(ln_eps >= 0.f))
     return fail(SVQ_E_SHAPE, "invalid LayerNorm eps");
-  if (residual && residual != y && x == y)
-    return fail(SVQ_E_SHAPE, "y must not alias x");
   Fusion f;
   f.ln_w = ln_weight;
   f.ln_b = ln_bias;

@@ -45,7 +45,10 @@ __global__ __launch_bounds__(kThreads) void beam_select_kernel(BeamSelectArgs a)
     const int64_t t = a.candidates[e];
     const int64_t f = (int64_t)b * a.vocab + (t < 0 ? 0 : t >= a.vocab ? a.vocab - 1 : t);
     fl[e] = f;
-    qv[e] = a.probs[a.compact ? e : f] / a.noise[f];
+    // A NaN race value (NaN probability, or 0 / 0) ranks last, as -inf: every
+    // round then has a winner among the `draws` <= beams * ncand entries.
+    const float qe = a.probs[a.compact ? e : f] / a.noise[f];
+    qv[e] = qe == qe ? qe : -INFINITY;
   }
   __syncthreads();
 
@@ -86,6 +89,10 @@ __global__ __launch_bounds__(kThreads) void beam_select_kernel(BeamSelectArgs a)
           bf = of;
           be = oe;
         }
+      }
+      if (be < 0) {  // unreachable with NaN ranked as -inf; keeps indexes in range
+        bf = fl[0];
+        be = 0;
       }
       // Every lane holds the winner; its owner marks it drawn.
 #pragma unroll
@@ -498,7 +505,7 @@ __global__ __launch_bounds__(kCandThreads) void cand_merge_kernel(BeamCandArgs a
 
 __global__ __launch_bounds__(kCandThreads) void beam_joint_kernel(BeamCandArgs a) {
   __shared__ float red[kCandThreads / 64];
-  __shared__ int nonzero;
+  __shared__ int nonzero, nans;
   const int tid = threadIdx.x;
   const int n = a.beams * a.kc;
   const float s = tid < n ? a.scores[tid] : -INFINITY;
@@ -506,16 +513,21 @@ __global__ __launch_bounds__(kCandThreads) void beam_joint_kernel(BeamCandArgs a
   const float e = s == -INFINITY ? 0.f : expf(s - m);
   const float total = block_reduce<kCandThreads>(e, false, red);
   const float p = e / total;
-  if (tid == 0) nonzero = 0;
+  if (tid == 0) nonzero = 0, nans = 0;
   __syncthreads();
-  const uint64_t mask = __ballot(tid < n && p != 0.f);
+  // Possible draws: probabilities > 0 (a NaN counts as none). A NaN
+  // probability makes the count -1: torch.multinomial rejects such input,
+  // and the caller raises its error instead of drawing.
+  const uint64_t mask = __ballot(tid < n && p > 0.f);
+  const uint64_t nan_mask = __ballot(tid < n && p != p);
   if ((tid & 63) == 0 && mask) atomicAdd(&nonzero, __popcll(mask));
+  if ((tid & 63) == 0 && nan_mask) atomicAdd(&nans, 1);
   if (tid < n) a.probs[tid] = p;
   __syncthreads();
   if (tid == 0) {
     int64_t any = 0;
     for (int r = 0; r < a.beams; ++r) any |= a.status[2 + r];
-    a.status[0] = nonzero;
+    a.status[0] = nans ? -1 : nonzero;
     a.status[1] = any;
   }
 }

@@ -23,7 +23,7 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 template <int OUT, int NV>
 __device__ __forceinline__ void store_values(void* out, int64_t first,
                                              const float (&v)[NV]) {
-  if constexpr (OUT == 0) {
+  if constexpr (OUT == kOutF32) {
     u32x4* o = reinterpret_cast<u32x4*>(reinterpret_cast<float*>(out) + first);
 #pragma unroll
     for (int i = 0; i < NV / 4; ++i)
@@ -35,7 +35,7 @@ __device__ __forceinline__ void store_values(void* out, int64_t first,
     uint16_t h[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      if constexpr (OUT == 1) {
+      if constexpr (OUT == kOutF16) {
         // The backend fuses product + conversion into v_fma_mixlo_f16 with a
         // +0 addend, which turns a -0 product into +0; the fp16 result always
         // carries the fp32 value's sign, so restore it from the fp32 bits.
@@ -172,9 +172,9 @@ template <int QT>
 static hipError_t dq_q(const uint8_t* q, const uint16_t* s, void* out,
                        int64_t nblocks, int out_dtype, hipStream_t stream) {
   switch (out_dtype) {
-    case 0: return dq<QT, 0>(q, s, out, nblocks, stream);
-    case 1: return dq<QT, 1>(q, s, out, nblocks, stream);
-    case 2: return dq<QT, 2>(q, s, out, nblocks, stream);
+    case kOutF16: return dq<QT, kOutF16>(q, s, out, nblocks, stream);
+    case kOutF32: return dq<QT, kOutF32>(q, s, out, nblocks, stream);
+    case kOutBF16: return dq<QT, kOutBF16>(q, s, out, nblocks, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -185,9 +185,9 @@ static hipError_t dq_rows_q(const uint8_t* q, const uint16_t* s,
                             int k, void* out, int out_dtype,
                             hipStream_t stream) {
   switch (out_dtype) {
-    case 0: return dq_rows<QT, 0>(q, s, ids, nids, nrows, k, out, stream);
-    case 1: return dq_rows<QT, 1>(q, s, ids, nids, nrows, k, out, stream);
-    case 2: return dq_rows<QT, 2>(q, s, ids, nids, nrows, k, out, stream);
+    case kOutF16: return dq_rows<QT, kOutF16>(q, s, ids, nids, nrows, k, out, stream);
+    case kOutF32: return dq_rows<QT, kOutF32>(q, s, ids, nids, nrows, k, out, stream);
+    case kOutBF16: return dq_rows<QT, kOutBF16>(q, s, ids, nids, nrows, k, out, stream);
   }
   return hipErrorInvalidValue;
 }

@@ -6,6 +6,10 @@
 
 namespace svq {
 
+// Output element types of the dequantize kernels: the C ABI's SVQ_F16,
+// SVQ_F32 and SVQ_BF16 codes.
+enum OutType { kOutF16 = 0, kOutF32 = 1, kOutBF16 = 2 };
+
 struct GemvArgs {
   const uint16_t* x;     // fp16 [m, k]
   const uint8_t* q;      // SoA payload

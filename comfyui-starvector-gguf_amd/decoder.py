@@ -1,16 +1,23 @@
-"""StarCoder2-style decoder harness that drives the quantized GEMV.
+"""StarCoder2-8B and GPTBigCode-1B decoder harnesses that drive the quantized GEMV.
 
-Restates the decode path of the reference's runtime_8b.py (Starcoder2Block
-:20-57, Starcoder2 :60-110), the KV-cache / graph machinery of
-runtime_shared.py (CachedDecoding :345-394) and its beam sampling
-(_penalize/_warp/_beam_sample :170-265). Every quantized linear is a
-`GGUFLinear` over SoA arrays, so each decode step runs the HIP GEMV 4 x layers
-+ 1 times (q, k and v are one fused linear: their SoA rows concatenated, a pure
-byte concatenation). On the GPU a decode step's attention (rotation of q and
-k, the cache write and grouped-query attention over the cache) is one HIP
-kernel per layer (`svq_decode_attention`), and the LayerNorms, GELU and
-residual adds run inside the GEMVs (`svq_gemv_fused`). Prefill, sampling and
-host decoding use PyTorch ops.
+Restates the decode paths of the reference's runtime_8b.py (Starcoder2Block
+:20-57, Starcoder2 :60-110) and runtime_1b.py (BigCodeBlock :17-49,
+GPTBigCode :52-91), the KV-cache / graph machinery of runtime_shared.py
+(CachedDecoding :345-394) and its beam sampling (_penalize/_warp/_beam_sample
+:170-265). Every quantized linear is a `GGUFLinear` over SoA arrays, so each
+decode step runs the HIP GEMV 4 x layers + 1 times (StarCoder2's q, k and v
+are one fused linear: their SoA rows concatenated, a pure byte
+concatenation; GPTBigCode's c_attn is one linear in the checkpoint already).
+
+Two ways to run a GPU decode step (`fused` on the model):
+- fused (the default): a layer's attention (rotation of q and k, the cache
+  write and the attention over the cache) is one HIP kernel
+  (`svq_decode_attention`), and the LayerNorms, GELU and residual adds run
+  inside the GEMVs (`svq_gemv_fused`): five HIP launches per layer;
+- as the reference runs it (`fused = False`): only the quantized linears are
+  HIP GEMVs; LayerNorm, attention, GELU and the residual adds are the
+  reference's torch ops.
+Prefill and host decoding use the reference's torch ops.
 
 Attention products are arranged so that no batched product takes a transposed
 view as its right operand: decode computes K @ q^T with a contiguous q^T, and
@@ -18,7 +25,6 @@ prefill multiplies by a contiguous K^T.
 """
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 
 import torch
@@ -54,6 +60,27 @@ class DecoderConfig:
         return self.hidden // self.heads
 
 
+@dataclass(frozen=True)
+class BigCodeConfig:
+    """GPTBigCode-1B (StarVector-1B) decoder shape: multi-query attention (one
+    key/value head), learned position embeddings, GELU MLP (runtime_1b.py:52-68
+    reads these from the GGUF's embedded config)."""
+    hidden: int = 2048
+    heads: int = 16
+    inner: int = 8192
+    layers: int = 24
+    vocab: int = 49152
+    context: int = 8192
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads
+
+    @property
+    def kv_heads(self) -> int:
+        return 1
+
+
 def random_soa(qtype: str, n: int, k: int, generator: torch.Generator, device) -> tuple:
     """Seeded synthetic SoA arrays: uniform payload bytes (uniform codes;
     Q8_0 int8 in [-127, 127]) and fp16 scales uniform in [1e-3, 2e-2]."""
@@ -86,10 +113,29 @@ def random_norm(width, generator, device):
     return norm
 
 
+def random_embedding(qtype, rows, width, generator, device):
+    table = GGUFEmbedding(rows, width)
+    table.set_soa(qtype, (rows, width), *random_soa(qtype, rows, width, generator, device))
+    table.output_dtype = torch.float16
+    return table
+
+
 def rotate(x, cos, sin):
     """Rotary embedding over rotated halves (runtime_8b.py:14-17)."""
     first, second = x.chunk(2, dim=-1)
     return x * cos + torch.cat((-second, first), dim=-1) * sin
+
+
+def decode_scores(keys, q, bias):
+    """Decode attention probabilities of one query row per (row, key/value
+    head): the reference's `baddbmm(bias, q, K^T, alpha=head_dim^-0.5)` and
+    fp32 softmax (runtime_8b.py:45-48; runtime_1b.py:45-47), computed as
+    K @ q^T with a contiguous q^T. keys [B, span, D], q [B, group, D];
+    returns [B, group, span] in q's dtype, for a `bmm` with V."""
+    hd = q.shape[-1]
+    qt = q.transpose(1, 2).contiguous()
+    scores = torch.bmm(keys, qt).transpose(1, 2) * hd ** -0.5 + bias
+    return torch.softmax(scores, -1, dtype=torch.float32).to(q.dtype).contiguous()
 
 
 class Starcoder2Block(nn.Module):
@@ -108,35 +154,35 @@ class Starcoder2Block(nn.Module):
         self.c_fc = random_linear(qtype, cfg.inner, cfg.hidden, generator, device)
         self.c_proj = random_linear(qtype, cfg.hidden, cfg.inner, generator, device)
 
-    def forward(self, x, cos, sin, keys, values, position=None, bias=None):
+    def forward(self, x, cos, sin, keys, values, position=None, bias=None, workspaces=None):
+        """Prefill (position None) or one decode step. With `workspaces` (the
+        decoding's own attention and GEMV workspaces) a GPU decode step runs
+        the fused HIP layer; without, the reference's torch ops."""
         cfg = self.cfg
         hd, heads, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
         rows, length, hidden = x.shape
-        if position is not None and x.is_cuda:
-            # A decode step on the GPU: five HIP launches per layer. The
-            # LayerNorms, GELU and residual adds run inside the GEMVs; the
-            # rotation, cache write and attention are one kernel (+ merge).
+        if position is not None and workspaces is not None:
+            # Five HIP launches per layer: the LayerNorms, GELU and residual
+            # adds run inside the GEMVs; the rotation, cache write and
+            # attention are one kernel (+ merge).
             x = x.reshape(rows, hidden)
             qkv = fused_linear(self.qkv_proj, x, norm=self.input_layernorm)
             out = torch.empty((rows, hidden), dtype=x.dtype, device=x.device)
-            workspace = native.attention_workspace(x.device, rows, heads, kvh, keys.shape[2])
             native.decode_attention(qkv, cos.view(-1), sin.view(-1), keys, values, position,
-                                    bias, out, heads, kvh, hd ** -0.5, workspace,
-                                    window=cfg.window if bias is None else 0)
+                                    None, out, heads, kvh, hd ** -0.5, workspaces["attention"],
+                                    window=cfg.window)
             x = fused_linear(self.o_proj, out, residual=x)
             h = fused_linear(self.c_fc, x, norm=self.post_attention_layernorm, gelu=True)
-            split = native.split_workspace(x.device, rows, hidden, cfg.inner,
-                                           self.c_proj._specs["weight"].qtype,
-                                           allocate=False, per_stream=False)
-            return fused_linear(self.c_proj, h, residual=x, workspace=split).view(rows, 1, hidden)
+            return fused_linear(self.c_proj, h, residual=x,
+                                workspace=workspaces["gemv"]).view(rows, 1, hidden)
         qkv = self.qkv_proj(self.input_layernorm(x))
         out = self.torch_attention(qkv, cos, sin, keys, values, position, bias)
         x = x + self.o_proj(out)
         return x + self.c_proj(F.gelu(self.c_fc(self.post_attention_layernorm(x)), approximate="tanh"))
 
     def torch_attention(self, qkv, cos, sin, keys, values, position=None, bias=None):
-        """The reference's attention ops (runtime_8b.py:38-55) in torch: prefill
-        on any device (position None) and decode on the host."""
+        """The reference's attention ops (runtime_8b.py:38-55) in torch:
+        prefill (position None) and decode on any device."""
         cfg = self.cfg
         hd, heads, kvh = cfg.head_dim, cfg.heads, cfg.kv_heads
         rows, length, _ = qkv.shape
@@ -152,12 +198,58 @@ class Starcoder2Block(nn.Module):
             return causal_attention(q, k, v, group).reshape(rows, length, hidden)
         keys.index_copy_(2, position, k)
         values.index_copy_(2, position, v)
-        # scores^T = K @ q^T per (row, kv head): [span, hd] @ [hd, group].
-        kb = keys.flatten(0, 1)
-        qt = q.reshape(rows * kvh, group, hd).transpose(1, 2).contiguous()
-        scores = torch.bmm(kb, qt).transpose(1, 2) * hd ** -0.5 + bias
-        probs = torch.softmax(scores, -1, dtype=torch.float32).to(qkv.dtype).contiguous()
+        probs = decode_scores(keys.flatten(0, 1), q.reshape(rows * kvh, group, hd), bias)
         return torch.bmm(probs, values.flatten(0, 1)).view(rows, 1, hidden)
+
+
+class BigCodeBlock(nn.Module):
+    """GPTBigCode multi-query block writing its keys/values into a fixed
+    cache (runtime_1b.py:17-49). The cache is [rows, 1, capacity, head_dim]:
+    the reference's [rows, capacity, head_dim] with its one key/value head
+    kept as a dimension, the layout of the StarCoder2 cache."""
+
+    def __init__(self, cfg: BigCodeConfig, qtype, generator, device):
+        super().__init__()
+        self.cfg = cfg
+        hd = cfg.head_dim
+        self.ln_1 = random_norm(cfg.hidden, generator, device)
+        self.c_attn = random_linear(qtype, cfg.hidden + 2 * hd, cfg.hidden, generator, device)
+        self.attn_proj = random_linear(qtype, cfg.hidden, cfg.hidden, generator, device)
+        self.ln_2 = random_norm(cfg.hidden, generator, device)
+        self.c_fc = random_linear(qtype, cfg.inner, cfg.hidden, generator, device)
+        self.c_proj = random_linear(qtype, cfg.hidden, cfg.inner, generator, device)
+
+    def forward(self, x, keys, values, position=None, bias=None, workspaces=None):
+        cfg = self.cfg
+        hd, heads = cfg.head_dim, cfg.heads
+        rows, length, hidden = x.shape
+        if position is not None and workspaces is not None:
+            # Five HIP launches per layer, as the StarCoder2 block: no
+            # rotation; the causal mask is the attention kernel's window,
+            # wider than the span.
+            x = x.reshape(rows, hidden)
+            qkv = fused_linear(self.c_attn, x, norm=self.ln_1)
+            out = torch.empty((rows, hidden), dtype=x.dtype, device=x.device)
+            native.decode_attention(qkv, None, None, keys, values, position, None, out, heads, 1,
+                                    hd ** -0.5, workspaces["attention"], window=keys.shape[2] + 1)
+            x = fused_linear(self.attn_proj, out, residual=x)
+            h = fused_linear(self.c_fc, x, norm=self.ln_2, gelu=True)
+            return fused_linear(self.c_proj, h, residual=x,
+                                workspace=workspaces["gemv"]).view(rows, 1, hidden)
+        q, k, v = self.c_attn(self.ln_1(x)).split((hidden, hd, hd), -1)
+        if position is None:
+            keys[:, 0, :length] = k
+            values[:, 0, :length] = v
+            q = q.view(rows, length, heads, hd).transpose(1, 2)
+            out = causal_attention(q, k[:, None], v[:, None], heads).reshape(rows, length, hidden)
+        else:
+            keys[:, 0].index_copy_(1, position, k)
+            values[:, 0].index_copy_(1, position, v)
+            # Multi-query: every head of a row attends the row's one key/value head.
+            probs = decode_scores(keys[:, 0], q.view(rows, heads, hd), bias)
+            out = torch.bmm(probs, values[:, 0]).view(rows, 1, hidden)
+        x = x + self.attn_proj(out)
+        return x + self.c_proj(F.gelu(self.c_fc(self.ln_2(x)), approximate="tanh"))
 
 
 def fused_linear(linear, x, norm=None, residual=None, gelu=False, workspace=None):
@@ -197,7 +289,47 @@ def causal_attention(q, k, v, group):
     return out.transpose(1, 2)
 
 
-class Starcoder2Decoder(nn.Module):
+class _Decoder(nn.Module):
+    """What the two decoders share: the host move, the decode workspaces and
+    the `fused` switch of GPU decode steps."""
+
+    # GPU decode steps run the fused HIP layer ops (True) or the reference's
+    # torch ops around the HIP GEMVs (False).
+    fused = True
+
+    def _norms_and_tables(self):
+        return [m for m in self.modules() if isinstance(m, (nn.LayerNorm, GGUFEmbedding))]
+
+    def to_host(self):
+        """Move to the CPU in fp32, the dtype the reference's loader uses on a
+        CPU (its GGUFLinear then runs the tiled dequantize + F.linear path)."""
+        self.to("cpu")
+        for module in self._norms_and_tables():
+            if isinstance(module, nn.LayerNorm):
+                module.float()
+            else:
+                module.output_dtype = torch.float32
+        return self
+
+    def decode_workspaces(self, rows, capacity, device):
+        """The fused decode step's workspaces, owned by one decoding: the
+        attention partials for the whole cache, and the K-split partial sums
+        of the longest rows (None when they run in one pass)."""
+        cfg = self.cfg
+        qtype = self.layers_list()[0].c_proj._specs["weight"].qtype
+        attention = torch.empty(native.attention_workspace_bytes(rows, cfg.heads, cfg.kv_heads,
+                                                                 capacity),
+                                dtype=torch.uint8, device=device)
+        need = native.gemv_workspace_bytes(rows, cfg.hidden, cfg.inner, qtype)
+        gemv = torch.empty(need, dtype=torch.uint8, device=device) if need else None
+        return {"attention": attention, "gemv": gemv}
+
+    def rope_table(self, capacity, dtype, device):
+        """Rotary tables of every cache slot, or None (no rotary embedding)."""
+        return None
+
+
+class Starcoder2Decoder(_Decoder):
     """StarCoder2-style decoder with a tied quantized embedding / head
     (runtime_8b.py:60-110), built from seeded synthetic SoA weights."""
 
@@ -205,14 +337,14 @@ class Starcoder2Decoder(nn.Module):
         super().__init__()
         self.cfg = cfg
         g = torch.Generator(device=device).manual_seed(seed)
-        self.embed_tokens = GGUFEmbedding(cfg.vocab, cfg.hidden)
-        hq = head_qtype or qtype
-        self.embed_tokens.set_soa(hq, (cfg.vocab, cfg.hidden), *random_soa(hq, cfg.vocab, cfg.hidden, g, device))
-        self.embed_tokens.output_dtype = torch.float16
+        self.embed_tokens = random_embedding(head_qtype or qtype, cfg.vocab, cfg.hidden, g, device)
         self.layers = nn.ModuleList([Starcoder2Block(cfg, qtype, g, device) for _ in range(cfg.layers)])
         self.norm = random_norm(cfg.hidden, g, device)
         self.lm_head = tied_head(self.embed_tokens)
         self.context = cfg.context
+
+    def layers_list(self):
+        return list(self.layers)
 
     def _rope(self, positions, dtype):
         hd = self.cfg.head_dim
@@ -222,18 +354,11 @@ class Starcoder2Decoder(nn.Module):
         angles = torch.cat((angles, angles), -1)
         return angles.cos().to(dtype), angles.sin().to(dtype)
 
+    def rope_table(self, capacity, dtype, device):
+        return self._rope(torch.arange(capacity, device=device), dtype)
+
     def embed(self, ids):
         return self.embed_tokens(ids)
-
-    def to_host(self):
-        """Move to the CPU in fp32, the dtype the reference's loader uses on a
-        CPU (its GGUFLinear then runs the tiled dequantize + F.linear path)."""
-        self.to("cpu")
-        for module in self.modules():
-            if isinstance(module, nn.LayerNorm):
-                module.float()
-        self.embed_tokens.output_dtype = torch.float32
-        return self
 
     def prefill(self, embeddings, rows, capacity):
         """Encode the prompt once (batch 1); its cache serves all `rows`."""
@@ -250,13 +375,15 @@ class Starcoder2Decoder(nn.Module):
         logits = self.lm_head(self.norm(x[:, -1]))
         return CachedDecoding(self, keys, values, length, kv), logits.expand(rows, -1)
 
-    def decode(self, tokens, position, keys, values, span, rope=None):
+    def decode(self, tokens, position, keys, values, span, rope=None, workspaces=None):
         """One token per row at `position`, attending the first `span` slots.
         `rope`: (cos, sin) tables over all cache slots (`_rope` of every
-        position, computed once), or None to compute this position's."""
-        if keys.is_cuda:
-            bias = None  # the attention kernel masks from the position and the window
-        else:
+        position, computed once), or None to compute this position's.
+        `workspaces`: the fused HIP step's (GPU), or None for the reference's
+        torch ops."""
+        fused = workspaces is not None and keys.is_cuda
+        bias = None  # the fused attention kernel masks from the position and the window
+        if not fused:
             slots = torch.arange(span, device=keys.device)
             hidden_slots = (slots > position) | (slots <= position - self.cfg.window)
             bias = torch.zeros(span, device=keys.device, dtype=keys.dtype).masked_fill_(
@@ -266,17 +393,77 @@ class Starcoder2Decoder(nn.Module):
         else:  # the same elementwise values, gathered
             cos, sin = rope[0].index_select(0, position), rope[1].index_select(0, position)
         x = self.embed_tokens(tokens)[:, None]
+        ws = workspaces if fused else None
         for layer, lk, lv in zip(self.layers, keys, values):
-            x = layer(x, cos, sin, lk[:, :, :span], lv[:, :, :span], position, bias)
-        if x.is_cuda:
+            x = layer(x, cos, sin, lk[:, :, :span], lv[:, :, :span], position, bias, ws)
+        if fused:
             return fused_linear(self.lm_head, x[:, 0], norm=self.norm)
         return self.lm_head(self.norm(x[:, 0]))
+
+
+class GPTBigCodeDecoder(_Decoder):
+    """GPTBigCode (StarVector-1B) decoder with a tied quantized token
+    embedding / head and learned position embeddings (runtime_1b.py:52-91),
+    built from seeded synthetic SoA weights. `embed_qtype` is the token and
+    position tables' type (the reference's converter keeps them Q8_0 in
+    Q4_0 / Q5_0 files, tools/starvector_safetensors_to_gguf.py:156-159)."""
+
+    def __init__(self, cfg: BigCodeConfig, qtype="Q4_0", embed_qtype=None, seed=0,
+                 device="cuda"):
+        super().__init__()
+        self.cfg = cfg
+        g = torch.Generator(device=device).manual_seed(seed)
+        eq = embed_qtype or qtype
+        self.wte = random_embedding(eq, cfg.vocab, cfg.hidden, g, device)
+        self.wpe = random_embedding(eq, cfg.context, cfg.hidden, g, device)
+        self.h = nn.ModuleList([BigCodeBlock(cfg, qtype, g, device) for _ in range(cfg.layers)])
+        self.ln_f = random_norm(cfg.hidden, g, device)
+        self.lm_head = tied_head(self.wte)
+        self.context = cfg.context
+
+    def layers_list(self):
+        return list(self.h)
+
+    def embed(self, ids):
+        return self.wte(ids)
+
+    def prefill(self, embeddings, rows, capacity):
+        """Encode the prompt once (batch 1); its cache serves all `rows`."""
+        cfg = self.cfg
+        length = embeddings.shape[1]
+        shape = (cfg.layers, rows, 1, capacity, cfg.head_dim)
+        kv = torch.zeros((2,) + shape, device=embeddings.device, dtype=embeddings.dtype)
+        keys, values = kv[0], kv[1]
+        x = embeddings + self.wpe(torch.arange(length, device=embeddings.device))
+        for block, lk, lv in zip(self.h, keys, values):
+            x = block(x, lk, lv)
+        logits = self.lm_head(self.ln_f(x[:, -1]))
+        return CachedDecoding(self, keys, values, length, kv), logits.expand(rows, -1)
+
+    def decode(self, tokens, position, keys, values, span, rope=None, workspaces=None):
+        """One token per row at `position`, attending the first `span` slots
+        (runtime_1b.py:84-91); `workspaces` as Starcoder2Decoder.decode."""
+        fused = workspaces is not None and keys.is_cuda
+        bias = None
+        if not fused:
+            slots = torch.arange(span, device=keys.device)
+            bias = torch.zeros(span, device=keys.device, dtype=keys.dtype).masked_fill_(
+                slots > position, float("-inf"))
+        x = (self.wte(tokens) + self.wpe(position))[:, None]
+        ws = workspaces if fused else None
+        for block, lk, lv in zip(self.h, keys, values):
+            x = block(x, lk[:, :, :span], lv[:, :, :span], position, bias, ws)
+        if fused:
+            return fused_linear(self.lm_head, x[:, 0], norm=self.ln_f)
+        return self.lm_head(self.ln_f(x[:, 0]))
 
 
 class CachedDecoding:
     """KV cache and graph-captured decode steps of one generation call
     (runtime_shared.py:345-394): one HIP graph per power-of-two span of at
-    least 512 slots, captured after an eager warm-up on a side stream."""
+    least 512 slots, captured after an eager warm-up on a side stream. The
+    decoding owns the workspaces its fused steps use, so graphs captured with
+    them stay valid for its whole life."""
 
     def __init__(self, model, keys, values, length, kv=None):
         """`kv`: the [2, ...] tensor whose halves are `keys` and `values`, if
@@ -286,24 +473,20 @@ class CachedDecoding:
         self.tokens = torch.zeros(keys.shape[1], dtype=torch.long, device=keys.device)
         self.position = torch.full((1,), length, dtype=torch.long, device=keys.device)
         self.graphs = {}
-        # RoPE angles of every cache slot, once (a decode step gathers its row).
-        self.rope = model._rope(torch.arange(keys.shape[3], device=keys.device), keys.dtype)
-        if keys.is_cuda:
-            # Allocated here, outside any capture, for the largest span; the
-            # decode steps reuse it.
-            cfg = model.cfg
-            native.attention_workspace(keys.device, keys.shape[1], cfg.heads, cfg.kv_heads,
-                                       keys.shape[3])
-            native.split_workspace(keys.device, keys.shape[1], cfg.hidden, cfg.inner,
-                                   model.layers[0].c_proj._specs["weight"].qtype,
-                                   per_stream=False)
+        capacity = keys.shape[3]
+        # Tables of every cache slot, once (a decode step gathers its row).
+        self.rope = model.rope_table(capacity, keys.dtype, keys.device)
+        self.workspaces = None
+        if keys.is_cuda and model.fused:
+            # Allocated here, outside any capture, for the largest span.
+            self.workspaces = model.decode_workspaces(keys.shape[1], capacity, keys.device)
 
     def span(self):
         return min(self.keys.shape[-2], max(512, 1 << self.length.bit_length()))
 
     def _decode(self, span):
         return self.model.decode(self.tokens, self.position, self.keys, self.values, span,
-                                 self.rope)
+                                 self.rope, self.workspaces)
 
     def step(self, tokens):
         """One decode step for `tokens` [rows] (None: already in self.tokens)."""
@@ -382,6 +565,15 @@ def warp(scores, temperature, top_p, keep):
         remove[..., -keep:] = False
         scores = scores.masked_fill(remove.scatter(-1, order, remove), float("-inf"))
     return scores
+
+
+def possible_draws(probs):
+    """Number of probabilities > 0 as a 0-d int64 tensor, or -1 when any is
+    NaN. The reference draws min(2 * beams, count_nonzero(probs)) samples
+    (runtime_shared.py:232); its torch.multinomial rejects NaN input, so a NaN
+    must reach multinomial rather than count as a possible draw."""
+    count = (probs > 0).sum()
+    return torch.where(torch.isnan(probs).any(), torch.full_like(count, -1), count)
 
 
 def stable_descending(values):
@@ -498,9 +690,9 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
     # when the top-k candidate set fits it.
     k = max(TOP_K, 2)
     kc = min(k + TIE_ROOM, vocab)
-    fused = on_gpu and k <= kc <= 64 and vocab <= 65536 and beams <= 8 and \
+    device_sampling = on_gpu and k <= kc <= 64 and vocab <= 65536 and beams <= 8 and \
         logits.dtype == torch.float16
-    if fused:
+    if device_sampling:
         cand = torch.empty((beams, kc), dtype=torch.long, device=device)
         cand_scores = torch.empty((beams, kc), device=device)
         cand_probs = torch.empty(beams * kc, device=device)
@@ -508,12 +700,12 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
         cand_ws = native.beam_candidates_workspace(beams, vocab, kc, device)
     for step in range(steps):
         seen_now, seen_next = seen_rows[step % 2], seen_rows[1 - step % 2]
-        if fused:
+        if device_sampling:
             native.beam_candidates(logits.contiguous(), seen_now, running_t, k, kc, 2,
                                    REPETITION_PENALTY, temperature, top_p, cand, cand_scores,
                                    cand_probs, status, cand_ws)
             noise = torch.empty((1, beams * vocab), device=device).exponential_()
-            possible, overflow = status[:2].tolist()
+            possible, overflow = status[:2].tolist()  # possible -1: a NaN probability
         else:
             penalized = penalize(torch.log_softmax(logits.float(), -1), seen_now[:, :vocab])
             log_probs, overflow, candidates = warp_candidates(penalized, temperature, top_p, 2,
@@ -523,20 +715,25 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
             noise = torch.empty_like(probs).exponential_()
             # One host read for the sample count and the tie check. Only the
             # candidates can have a non-zero probability: count those.
-            possible = torch.count_nonzero(probs.view(beams, vocab).gather(1, candidates))
+            possible = possible_draws(probs.view(beams, vocab).gather(1, candidates))
             possible, overflow = torch.stack((possible, overflow.long())).tolist()
         if overflow:
             penalized = penalize(torch.log_softmax(logits.float(), -1), seen_now[:, :vocab])
             log_probs = warp(penalized, temperature, top_p, 2)
             scores = (log_probs + running_t[:, None]).view(1, -1)
             probs = scores.softmax(-1)
-            possible = int(torch.count_nonzero(probs))
+            possible = int(possible_draws(probs))
         draws = min(keep, possible)
-        if draws < 1:  # no possible continuation: torch.multinomial's own error, as the reference
-            torch.multinomial(cand_probs.view(1, -1) if fused and not overflow else probs, draws)
+        if draws < 1:
+            # No possible continuation, or a NaN probability: torch.multinomial
+            # raises its own error, as in the reference (which draws
+            # min(keep, count_nonzero) samples from the same probabilities).
+            torch.multinomial(cand_probs.view(1, -1) if device_sampling and not overflow else probs,
+                              max(draws, 1) if possible < 0 else draws)
+            raise RuntimeError("beam sampling: no possible continuation")
         parents, tokens = history[step, 0], history[step, 1]
         if on_gpu and not overflow and draws >= 1:
-            if fused:
+            if device_sampling:
                 native.beam_select(cand_probs, noise, cand_scores, cand, draws, seen_now,
                                    seen_next, running_t, parents, tokens, decoding.tokens)
             else:
@@ -574,3 +771,45 @@ def beam_steps(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9, 
         best.append(tokens_all[step][beam])
         beam = parents_all[step][beam]
     return best[::-1], running_t.tolist()
+
+
+def beam_steps_reference(decoder, embeddings, steps, beams=2, temperature=1.5, top_p=0.9,
+                         capacity=None, on_prefill=None, on_step=None):
+    """The reference's beam sampling loop (runtime_shared.py:214-265) for a
+    fixed number of decode steps, as it runs it: the whole-vocabulary warpers
+    (`warp`), `torch.multinomial` over min(2 * beams, count_nonzero) samples,
+    the survivors chosen with Python's `sorted` on the host, a host list of
+    parents for the cache reorder, then the next step. No end-of-sequence
+    token stops it (there is no tokenizer), so the finished-beam bookkeeping
+    never runs. Returns (best token sequence, running scores)."""
+    keep = 2 * beams
+    capacity = capacity or embeddings.shape[1] + steps + 1
+    decoding, logits = decoder.prefill(embeddings, beams, capacity)
+    if on_prefill is not None:
+        on_prefill()
+    device, vocab = logits.device, logits.shape[-1]
+    running = [[] for _ in range(beams)]
+    running_scores = [0.0] + [-1e9] * (beams - 1)
+    seen = torch.zeros((beams, vocab), dtype=torch.bool, device=device)
+    rows = torch.arange(beams, device=device)
+    for step in range(steps):
+        log_probs = warp(penalize(torch.log_softmax(logits.float(), -1), seen), temperature,
+                         top_p, 2)
+        scores = (log_probs + torch.tensor(running_scores, device=device)[:, None]).view(1, -1)
+        probs = scores.softmax(-1)
+        picks = torch.multinomial(probs, min(keep, int(torch.count_nonzero(probs))))
+        picked = scores.gather(1, picks)[0].tolist()
+        parents, tokens = zip(*(divmod(pick, vocab) for pick in picks[0].tolist()))
+        order = sorted(range(len(picked)), key=picked.__getitem__, reverse=True)[:beams]
+        running_scores = [picked[j] for j in order] + [-1e9] * (beams - len(order))
+        order += [order[0]] * (beams - len(order))
+        running = [running[parents[j]] + [tokens[j]] for j in order]
+        selected = torch.tensor([parents[j] for j in order], device=device)
+        next_tokens = torch.tensor([tokens[j] for j in order], device=device)
+        seen = seen[selected]
+        seen[rows, next_tokens] = True
+        decoding.reorder([parents[j] for j in order])
+        logits = decoding.step(next_tokens)
+        if on_step is not None:
+            on_step(step + 1)
+    return running[0], running_scores

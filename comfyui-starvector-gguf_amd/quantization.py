@@ -15,6 +15,7 @@ from contextlib import contextmanager
 from contextvars import ContextVar
 from dataclasses import dataclass
 import logging
+import os
 
 import numpy as np
 import torch
@@ -272,9 +273,15 @@ def _soa_gemm(inp, qbytes, scales_u8, spec, bias, out):
 def _fused_soa_linear(x, qbytes, scale_bits, spec, bias):
     """GPU fp16 dispatch (reference quantization.py:286-323): the fused HIP
     GEMV for up to GEMV_MAX_ROWS rows, dequantize + GEMM beyond. Returns None
-    only for inputs this path does not take (CPU tensors, non-fp16
-    activations), as the reference does; kernel errors propagate."""
-    if x.device.type != "cuda" or x.dtype != torch.float16 or x.numel() % spec.shape[1]:
+    -- the caller then runs the tiled dequantize + F.linear path -- for
+    inputs this path does not take (CPU tensors, non-fp16 activations) and
+    when the reference's switch STARVECTOR_DISABLE_TRITON is "1" (off by
+    default), as the reference does. Unlike the reference, a kernel error
+    propagates instead of being logged and answered with that path: a failed
+    launch is an invalid argument or a broken device, not a reason to change
+    arithmetic silently."""
+    if (x.device.type != "cuda" or os.getenv("STARVECTOR_DISABLE_TRITON") == "1" or
+            x.dtype != torch.float16 or x.numel() % spec.shape[1]):
         return None
     nrows = x.numel() // spec.shape[1]
     n, k = spec.shape

@@ -34,16 +34,17 @@
 extern "C" {
 #endif
 
-#define SVQ_ABI_VERSION 2
+#define SVQ_ABI_VERSION 3
 
 /* Quantization codes: the reference's kernel codes (quantization.py:120). */
 #define SVQ_Q4_0 4
 #define SVQ_Q5_0 5
 #define SVQ_Q8_0 8
 
-/* Element types of dequantized or GEMV outputs. */
-#define SVQ_F32 0
-#define SVQ_F16 1
+/* Element types of dequantized or GEMV outputs. SVQ_F16 and SVQ_F32 are 0
+   and 1, so a `y_is_fp32` / `out_is_fp32` flag passes as one of them. */
+#define SVQ_F16 0
+#define SVQ_F32 1
 #define SVQ_BF16 2
 
 #define SVQ_MAX_ROWS 8 /* largest M of svq_gemv */
@@ -80,15 +81,16 @@ const char *svq_last_error(void);
  *   x     fp16 [m, k] row-major
  *   q, s  SoA payload and fp16 scale bits of the n x k matrix
  *   bias  fp16 [n] or NULL
- *   y     [m, n] row-major, fp16 (y_dtype SVQ_F16, as the reference stores)
- *         or fp32 (SVQ_F32)
+ *   y     [m, n] row-major: fp16 with y_is_fp32 = 0 (SVQ_F16, as the
+ *         reference stores), fp32 with y_is_fp32 = 1 (SVQ_F32); other values
+ *         are rejected (SVQ_E_DTYPE). y may share no byte with x, q, s or bias.
  * Each block's integer dot product is accumulated in fp32 and multiplied by
  * its scale once (quantization.py:199, 215); bias is added in fp32 before the
  * final rounding.
  */
 int svq_gemv(const void *x, const uint8_t *q, const uint16_t *s,
              const uint16_t *bias, void *y, int m, int n, int k, int qtype,
-             int y_dtype, void *stream);
+             int y_is_fp32, void *stream);
 
 /*
  * svq_gemv with the decoder-layer ops around it fused in; y is fp16:
@@ -105,7 +107,8 @@ int svq_gemv(const void *x, const uint8_t *q, const uint16_t *s,
  *   activation  SVQ_ACT_NONE or SVQ_ACT_GELU_TANH, applied to the rounded
  *             product and rounded again
  *   residual  fp16 [m, n] added last (then rounded), or NULL; may be y itself
- *             (in place); y must not alias x.
+ *             (in place). Otherwise y may share no byte with any input (x,
+ *             q, s, bias, LayerNorm parameters, residual): SVQ_E_SHAPE.
  * With a LayerNorm, x must fit the streaming kernels' LDS staging (m * k * 2
  * bytes plus offset sums within 156 KB), otherwise SVQ_E_SHAPE.
  */
@@ -125,8 +128,9 @@ int svq_gemv_fused(const void *x, const uint8_t *q, const uint16_t *s,
  * Replaces the same reference calls as svq_gemv / svq_gemv_fused
  * (quantization.py:232-265; runtime_8b.py:57 for c_proj with its residual).
  *   workspace  device memory, 16-byte aligned, or NULL; calls sharing one
- *              must not overlap (same stream, or ordered by events)
- * y is fp16.
+ *              must not overlap (same stream, or ordered by events); it may
+ *              share no byte with y or an input
+ * y is fp16, with the overlap rules of svq_gemv_fused.
  */
 int svq_gemv_split(const void *x, const uint8_t *q, const uint16_t *s,
                    const uint16_t *bias, void *y, int m, int n, int k, int qtype,
@@ -152,8 +156,9 @@ int svq_gemv_plan(int m, int n, int k, int qtype, int32_t *plan);
 
 /*
  * out[b * 32 + j] = weight j of block b, for b < nblocks, rounded from the
- * exact fp32 product to out_dtype (SVQ_F32 / SVQ_F16 / SVQ_BF16, round to
- * nearest even). Replaces `dequantize_soa` (quantization.py:93-105) on the GPU.
+ * exact fp32 product to out_dtype: SVQ_F16 (0) or SVQ_F32 (1), i.e. an
+ * out_is_fp32 flag, or SVQ_BF16 (2); round to nearest even. Replaces
+ * `dequantize_soa` (quantization.py:93-105) on the GPU.
  */
 int svq_dequant(const uint8_t *q, const uint16_t *s, void *out,
                 int64_t nblocks, int qtype, int out_dtype, void *stream);
@@ -273,7 +278,8 @@ int svq_beam_select(const float *probs, const float *noise, const float *scores,
  *   candidates  int64 [beams, kc] out: token ids, value descending, token ascending
  *   scores      fp32 [beams, kc] out: warped log-prob + running (-inf if removed)
  *   probs       fp32 [beams * kc] out: joint softmax of scores
- *   status      int64 [2 + beams] out: number of non-zero probs; 1 if any row
+ *   status      int64 [2 + beams] out: number of probs > 0, or -1 if any prob
+ *               is NaN (torch.multinomial rejects such input); 1 if any row
  *               overflows (its kc-th largest value equals its k-th: the
  *               candidates may then miss tokens the reference keeps, and the
  *               caller must warp the whole vocabulary); then the flag per row

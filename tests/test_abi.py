@@ -36,19 +36,32 @@ def test_library_exports_every_declared_function():
 
 
 def test_abi_version():
-    assert native.load().svq_abi_version() == native.ABI_VERSION == 2
+    assert native.load().svq_abi_version() == native.ABI_VERSION == 3
 
 
 FAKE = 1 << 20  # a 16-byte aligned non-null address; never dereferenced
+# Distinct fake arrays, 1 MiB apart: no two of them overlap at the sizes used.
+X, Q, S, Y, B, W, R = (FAKE * i for i in range(2, 9))
+
+
+def test_dtype_codes_are_the_fp32_flags():
+    """SVQ_F16 = 0 and SVQ_F32 = 1: svq_gemv's y_is_fp32 and svq_dequant's
+    out_is_fp32 flags (the boundary's suggested signatures) are the codes."""
+    text = HEADER.read_text()
+    codes = dict(re.findall(r"#define (SVQ_F16|SVQ_F32|SVQ_BF16) (\d+)", text))
+    assert codes == {"SVQ_F16": "0", "SVQ_F32": "1", "SVQ_BF16": "2"}
+    assert native.DTYPE_CODE == {__import__("torch").float16: 0, __import__("torch").float32: 1,
+                                 __import__("torch").bfloat16: 2}
+    assert re.search(r"int svq_gemv\(.*?int y_is_fp32, void \*stream\);", text, re.S)
 
 
 def gemv(**kw):
-    args = dict(x=FAKE, q=FAKE, s=FAKE, bias=None, y=FAKE, m=1, n=8, k=64, qtype=4,
-                y_dtype=1, stream=None)
+    args = dict(x=X, q=Q, s=S, bias=None, y=Y, m=1, n=8, k=64, qtype=4, y_is_fp32=0,
+                stream=None)
     args.update(kw)
     lib = native.load()
     return lib.svq_gemv(args["x"], args["q"], args["s"], args["bias"], args["y"], args["m"],
-                        args["n"], args["k"], args["qtype"], args["y_dtype"], args["stream"])
+                        args["n"], args["k"], args["qtype"], args["y_is_fp32"], args["stream"])
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -56,9 +69,12 @@ def gemv(**kw):
     (dict(m=0), -2), (dict(m=9), -2), (dict(n=0), -2), (dict(k=0), -2), (dict(k=48), -2),
     (dict(k=1 << 25), -5), (dict(n=(1 << 30) + 1), -5),
     (dict(x=None), -3), (dict(q=None), -3), (dict(s=None), -3), (dict(y=None), -3),
-    (dict(y_dtype=2), -4), (dict(y_dtype=7), -4),
-    (dict(x=FAKE + 8), -6), (dict(q=FAKE + 4), -6), (dict(q=FAKE + 4, qtype=5), None),
-    (dict(s=FAKE + 1), -6), (dict(bias=FAKE + 1), -6), (dict(y=FAKE + 1), -6),
+    (dict(y_is_fp32=2), -4), (dict(y_is_fp32=7), -4), (dict(y_is_fp32=-1), -4),
+    (dict(x=X + 8), -6), (dict(q=Q + 4), -6), (dict(q=Q + 4, qtype=5), None),
+    (dict(s=S + 1), -6), (dict(bias=B + 1), -6), (dict(y=Y + 1), -6),
+    # y may share no byte with an input (workgroups write y while others read)
+    (dict(y=X), -2), (dict(y=X + 112), -2), (dict(x=Y - 112), -2), (dict(y=Q + 240), -2),
+    (dict(y=S + 16), -2), (dict(bias=Y + 8), -2),
 ])
 def test_gemv_rejects_bad_arguments(kw, code):
     if code is None:
@@ -177,7 +193,7 @@ def test_cache_reorder_empty_length_is_a_no_op():
 
 
 def gemv_fused(**kw):
-    args = dict(x=FAKE, q=FAKE, s=FAKE, bias=None, y=FAKE + 1024, m=2, n=8, k=64, qtype=4,
+    args = dict(x=X, q=Q, s=S, bias=None, y=Y, m=2, n=8, k=64, qtype=4,
                 ln_w=None, ln_b=None, eps=1e-5, res=None, act=0)
     args.update(kw)
     return native.load().svq_gemv_fused(
@@ -187,12 +203,13 @@ def gemv_fused(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(act=2), -4), (dict(ln_w=FAKE + 2), -6), (dict(ln_b=FAKE + 8), -6),
-    (dict(res=FAKE + 1), -6), (dict(ln_w=FAKE, eps=-1.0), -2),
-    (dict(y=FAKE, res=FAKE + 64), -2),
+    (dict(act=2), -4), (dict(ln_w=W + 2), -6), (dict(ln_b=W + 8), -6),
+    (dict(res=R + 1), -6), (dict(ln_w=W, eps=-1.0), -2),
+    (dict(y=X, res=R), -2), (dict(y=X + 64, res=X + 64), -2), (dict(ln_w=Y - 64), -2),
+    (dict(ln_b=Y + 16), -2), (dict(res=Y + 2), -2), (dict(res=Y - 30), -2),
     (dict(qtype=3), -1), (dict(m=9), -2), (dict(k=40), -2), (dict(x=None), -3),
     # x of 8 rows x 18432 does not fit the LDS staging the LayerNorm needs
-    (dict(m=8, k=18432, n=64, ln_w=FAKE), -2),
+    (dict(m=8, k=18432, n=64, ln_w=W), -2),
 ])
 def test_gemv_fused_rejects_bad_arguments(kw, code):
     assert gemv_fused(**kw) == code
@@ -200,8 +217,8 @@ def test_gemv_fused_rejects_bad_arguments(kw, code):
 
 
 def gemv_split(**kw):
-    args = dict(x=FAKE, q=FAKE, s=FAKE, bias=None, y=FAKE + 1024, m=2, n=8, k=64, qtype=4,
-                res=None, act=0, ws=FAKE, ws_bytes=1 << 20)
+    args = dict(x=X, q=Q, s=S, bias=None, y=Y, m=2, n=8, k=64, qtype=4,
+                res=None, act=0, ws=FAKE * 9, ws_bytes=1 << 16)
     args.update(kw)
     return native.load().svq_gemv_split(
         args["x"], args["q"], args["s"], args["bias"], args["y"], args["m"], args["n"],
@@ -209,8 +226,11 @@ def gemv_split(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(act=2), -4), (dict(res=FAKE + 1), -6), (dict(ws=FAKE + 8), -6),
-    (dict(y=FAKE, res=FAKE + 64), -2), (dict(ws_bytes=-1), -7),
+    (dict(act=2), -4), (dict(res=R + 1), -6), (dict(ws=FAKE * 9 + 8), -6),
+    (dict(y=X, res=R), -2), (dict(res=Y + 4), -2), (dict(ws_bytes=-1), -7),
+    # the workspace is written: it may share no byte with y or an input
+    (dict(ws=Y - 64, ws_bytes=128), -2), (dict(ws=X + 16), -2), (dict(ws=Q), -2),
+    (dict(ws=R - 16, ws_bytes=32, res=R), -2),
     (dict(qtype=3), -1), (dict(m=9), -2), (dict(k=40), -2), (dict(x=None), -3),
 ])
 def test_gemv_split_rejects_bad_arguments(kw, code):

@@ -283,3 +283,85 @@ def test_embedding_gpu(cuda_device, qtype):
     assert torch.equal(got.cpu(), dense[selected.cpu()])
     emb.output_dtype = torch.float16
     assert torch.equal(emb(selected).cpu(), dense[selected.cpu()].half())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("m", (2, 4, 8))
+def test_soa_gemv_long_rows_split_k_against_oracle(cuda_device, qtype, m):
+    """`soa_gemv` itself on the 8B c_proj shape (4608 x 18432), where fp16
+    output splits K across workgroups through the per-stream workspace
+    (svq_gemv_split: fp32 partial sums per slice, added in slice order by
+    the finish kernel): the fp64 oracle at the 1e-3 bar of
+    tools/tune_kernels.py:83. fp32 output runs the one-pass kernel and meets
+    the 1e-5 bar of the fp32 GEMV tests."""
+    n, k = 4608, 18432
+    print(f"soa_gemv split-K {qtype} M={m}", flush=True)
+    q, s = orc.synthetic_soa(qtype, n, k, seed=40 + m)
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    bias = (0.02 * rng.standard_normal(n)).astype(np.float16)
+    ref = orc.gemv_ref(x, q, s, qtype, n, k, bias)
+    assert quant._native.gemv_workspace_bytes(m, n, k, qtype) > 0  # this shape splits
+    qt = torch.from_numpy(q).to(cuda_device)
+    st = torch.from_numpy(s).to(cuda_device).view(torch.float16)
+    xt = torch.from_numpy(x).to(cuda_device)
+    bt = torch.from_numpy(bias).to(cuda_device)
+    out16 = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda_device)
+    soa_gemv(xt, qt, st, out16, qtype, bias=bt)
+    out32 = torch.full((m, n), float("nan"), dtype=torch.float32, device=cuda_device)
+    soa_gemv(xt, qt, st, out32, qtype, bias=bt)
+    torch.cuda.synchronize()
+    assert orc.rel_err(out16.float().cpu().numpy(), ref) <= 1e-3
+    assert orc.rel_err(out32.cpu().numpy(), ref) <= 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("dtype", (torch.float32, torch.float16, torch.bfloat16))
+def test_dequantize_aos_on_gpu_bit_exact(cuda_device, qtype, dtype):
+    """`dequantize` of GGUF AoS blocks already on the GPU (split to SoA, then
+    the HIP decode; quantization.py:50-65) equals the oracle's exact fp32
+    product, rounded once to `dtype`."""
+    n, k = 257, 96
+    raw = orc.packed_matrix(qtype, n, k, seed=11)
+    want = torch.from_numpy(orc.dequantize_aos(raw, qtype, (n, k))).to(dtype)
+    got = dequantize(torch.from_numpy(raw).to(cuda_device), qtype, (n, k), dtype)
+    assert got.device.type == "cuda" and got.dtype == dtype and got.shape == (n, k)
+    assert torch.equal(got.cpu().view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       want.view(torch.int16 if dtype != torch.float32 else torch.int32))
+    with pytest.raises(ValueError):
+        dequantize(torch.from_numpy(raw[:-1]).to(cuda_device), qtype, (n, k), dtype)
+
+
+@pytest.mark.gpu
+def test_no_fallback_by_default_and_reference_switch(cuda_device, monkeypatch):
+    """Without STARVECTOR_DISABLE_TRITON the GPU fp16 path is the fused HIP
+    GEMV and never the tiled dequantize + F.linear fallback; with the
+    reference's switch set to "1" it is the fallback (quantization.py:286-291,
+    390-407), with the same result to the GEMV's bar."""
+    m, n, k = 2, 96, 256
+    layer = GGUFLinear(k, n)
+    layer.set_gguf("weight", packed("Q5_0", n, k))
+    layer = layer.to(cuda_device)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(3)).half().to(cuda_device)
+    monkeypatch.delenv("STARVECTOR_DISABLE_TRITON", raising=False)
+    real_dequant = quant.dequantize_soa
+
+    def no_dequant(*args, **kwargs):
+        raise AssertionError("the tiled fallback ran")
+
+    monkeypatch.setattr(quant, "dequantize_soa", no_dequant)
+    fused = layer(x)
+    monkeypatch.setattr(quant, "dequantize_soa", real_dequant)
+    monkeypatch.setenv("STARVECTOR_DISABLE_TRITON", "1")
+
+    def no_gemv(*args, **kwargs):
+        raise AssertionError("the fused GEMV ran")
+
+    monkeypatch.setattr(quant._native, "gemv", no_gemv)
+    tiled = layer(x)
+    w = orc.dequantize_aos(np.asarray(packed("Q5_0", n, k).data), "Q5_0", (n, k))
+    ref = x.double().cpu().numpy() @ w.astype(np.float64).T
+    assert orc.rel_err(fused.float().cpu().numpy(), ref) <= 1e-3
+    assert orc.rel_err(tiled.float().cpu().numpy(), ref) <= 1e-3
