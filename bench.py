@@ -10,15 +10,20 @@ scales + fp16 x + fp16 y + fp16 bias.
 
 Measurement: seeded synthetic weights resident in HBM. Every matrix exists in
 8 distinct copies (>= 2.4 GB per pass rotation), so each launch reads weights
-that the 256 MB Infinity Cache no longer holds; the timed region replays a HIP
-graph of 8 passes, bracketed by HIP events on the launch stream and device
-synchronization. The `roofline` object is for the dominant launch (lm_head),
-timed the same way in its own graph. `sweep` holds every GEMV configuration
-(1B Q4_0 shapes, 8B Q5_0 shapes, 8192x2048 Q8_0, the beam-width sweep),
-each as the median of 5 trials over >= 1 GiB of rotating copies.
-`cpu_baseline` times the reference's CPU path (tiled fp32 dequantize +
-F.linear, restated in oracle/) on the host cores for one pass of the same
-step.
+that the 256 MB Infinity Cache no longer holds; step i uses copy i % 8. After
+exactly W untimed steps, a HIP graph of exactly K steps is replayed in 5
+trials, each bracketed by HIP events on the launch stream and device
+synchronization; `value` is from the median trial. The `roofline` object is
+for the dominant launch (lm_head), timed the same way in its own graph.
+`sweep` holds every GEMV configuration (1B Q4_0 shapes, 8B Q5_0 shapes,
+8192x2048 Q8_0, the beam-width sweep), each as the median of 5 trials over
+>= 1 GiB of rotating copies. `cpu_baseline` times the reference's CPU path
+(tiled fp32 dequantize + F.linear, restated in oracle/) on the host cores for
+one pass of the same step, and `cpu_sweep` every sweep configuration.
+`decode` holds the decode loops: the StarCoder2-8B-style loop (32 layers,
+Q4_0, beam 2) and the GPTBigCode-1B loop (24 layers, Q4_0 linears, Q8_0
+tables, beam 2), each run as the reference specifies it (torch attention,
+LayerNorm and sampling around the HIP GEMVs) and fused.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
 """
@@ -397,11 +402,22 @@ def committed_traffic(name, n, k):
     return None
 
 
-def cpu_baseline(seconds_budget=20.0):
+def host_cores():
+    """(threads the CPU baselines use, the host's CPU count): every CPU this
+    process may run on (its affinity mask, which on a GPU box is the share
+    of the host its job is given), and os.cpu_count() for the record."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return usable, os.cpu_count()
+
+
+def cpu_baseline():
     """The reference's CPU path (tiled fp32 dequantize + F.linear), restated
     in oracle/, for one pass of the step at batch 2, timed on this host."""
     from oracle import soa_oracle as orc
-    threads = min(os.cpu_count() or 1, 16)
+    threads, host_cpus = host_cores()
     torch.set_num_threads(threads)
     total_bytes, elapsed = 0, 0.0
     per = []
@@ -421,95 +437,170 @@ def cpu_baseline(seconds_budget=20.0):
         total_bytes += algorithmic_bytes(STEP_QTYPE, n, k, STEP_M, bias)
         elapsed += t
     return {"value": round(total_bytes / elapsed / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+            "host_cpus": host_cpus, "kind": "port",
             "sample": "one pass of the Q5_0 batch-2 8B step (5 GEMVs) through the reference's "
                       "CPU path (tiled fp32 dequantize + F.linear), median of 3",
             "ms_per_step": round(elapsed * 1e3, 1), "per_shape": per}
 
 
-# StarCoder2-8B-style decode loop: 32 layers, Q4_0 weights, beam 2, a
-# 1024-token prefill whose first 576 vectors are the seeded vision prompt,
-# then a fixed number of decode steps (random end-of-sequence tokens cannot
-# stop it).
+def cpu_sweep():
+    """Every `sweep` configuration (configs 1-4) through the reference's CPU
+    path on the host cores: ms per GEMV (median of 3 after one warm-up) and
+    GB/s of algorithmic bytes."""
+    from oracle import soa_oracle as orc
+    threads, host_cpus = host_cores()
+    torch.set_num_threads(threads)
+    rows, mats = [], {}
+    for cfg_name, qtype, n, k, m, bias in sweep_cases():
+        if (qtype, n, k) not in mats:
+            mats.clear()  # one matrix resident at a time (cases are grouped by shape)
+            q, s = orc.synthetic_soa(qtype, n, k, seed=n + k)
+            mats[qtype, n, k] = (torch.from_numpy(q), torch.from_numpy(s))
+        qt, st = mats[qtype, n, k]
+        gen = torch.Generator().manual_seed(m)
+        x = torch.randn((m, k), generator=gen)
+        b = torch.randn(n, generator=gen) if bias else None
+        orc.tiled_linear_cpu(x, qt, st, qtype, n, k, b)
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            orc.tiled_linear_cpu(x, qt, st, qtype, n, k, b)
+            runs.append(time.perf_counter() - t0)
+        t = statistics.median(runs)
+        nbytes = algorithmic_bytes(qtype, n, k, m, bias)
+        rows.append({"config": cfg_name, "qtype": qtype, "n": n, "k": k, "m": m,
+                     "ms": round(t * 1e3, 3), "gbs": round(nbytes / t / 1e9, 3)})
+    return {"cores": threads, "host_cpus": host_cpus, "kind": "port",
+            "sample": "each sweep configuration once through the reference's CPU path (tiled "
+                      "fp32 dequantize + F.linear), median of 3 after a warm-up",
+            "cases": rows}
+
+
+# Decode loops. StarCoder2-8B-style: 32 layers, Q4_0 weights, beam 2, a
+# 1024-token prefill whose first 576 vectors are the seeded vision prompt
+# (SigLIP's 576 image tokens), then a fixed number of decode steps (random
+# end-of-sequence tokens cannot stop it). GPTBigCode-1B: 24 layers, Q4_0
+# linears with Q8_0 token / position tables (as the reference's converter
+# writes Q4_0 files), the same loop with a 257-vector vision prompt (CLIP's
+# 257 image tokens).
 DECODE = {"qtype": "Q4_0", "beams": 2, "prompt": 576, "prefill": 1024, "steps": 512}
+DECODE_1B = {"qtype": "Q4_0", "embed_qtype": "Q8_0", "beams": 2, "prompt": 257, "prefill": 1024,
+             "steps": 512}
 
 
-def decode_model(dev):
-    from starvector_amd.decoder import DecoderConfig, Starcoder2Decoder
-    cfg = DecoderConfig()
-    return cfg, Starcoder2Decoder(cfg, qtype=DECODE["qtype"], seed=0, device=dev)
+def decode_model(dev, family="8b"):
+    from starvector_amd.decoder import (BigCodeConfig, DecoderConfig, GPTBigCodeDecoder,
+                                        Starcoder2Decoder)
+    if family == "8b":
+        cfg = DecoderConfig()
+        return cfg, Starcoder2Decoder(cfg, qtype=DECODE["qtype"], seed=0, device=dev)
+    cfg = BigCodeConfig()
+    return cfg, GPTBigCodeDecoder(cfg, qtype=DECODE_1B["qtype"],
+                                  embed_qtype=DECODE_1B["embed_qtype"], seed=0, device=dev)
 
 
-def decode_prompt(cfg, dev, length, dtype=torch.float16):
-    """The seeded vision prompt (576 fp16 N(0,1) vectors), extended with
+def decode_prompt(cfg, dev, length, vision, dtype=torch.float16):
+    """The seeded vision prompt (`vision` fp16 N(0,1) vectors), extended with
     further seeded vectors to `length` prefill tokens."""
     g = torch.Generator(device=dev).manual_seed(1)
-    vision = torch.randn((1, min(length, DECODE["prompt"]), cfg.hidden), generator=g, device=dev)
-    extra = torch.randn((1, max(0, length - DECODE["prompt"]), cfg.hidden), generator=g, device=dev)
-    return torch.cat((vision, extra), 1).to(dtype)
+    head = torch.randn((1, min(length, vision), cfg.hidden), generator=g, device=dev)
+    extra = torch.randn((1, max(0, length - vision), cfg.hidden), generator=g, device=dev)
+    return torch.cat((head, extra), 1).to(dtype)
 
 
-def run_decode(model, emb, steps, sync):
-    """Beam-2 decode of `steps` steps; returns wall-clock marks (seconds)."""
-    from starvector_amd.decoder import beam_steps
+def run_decode(model, emb, steps, sync, beams, as_specified=False):
+    """Beam decode of `steps` steps; returns wall-clock marks (seconds). As
+    specified: the reference's loop (whole-vocabulary torch warpers,
+    torch.multinomial, host survivor selection) over the decoder's torch
+    attention / LayerNorm path; otherwise the fused loop."""
+    from starvector_amd.decoder import beam_steps, beam_steps_reference
     marks = {}
 
     def mark(key):
         sync()
         marks[key] = time.perf_counter()
 
+    loop = beam_steps_reference if as_specified else beam_steps
+    model.fused = not as_specified
     torch.manual_seed(0)
     with torch.inference_mode():
         mark("start")
-        beam_steps(model, emb, steps, DECODE["beams"], on_prefill=lambda: mark("prefill"),
-                   on_step=lambda i: mark("first") if i == 1 else None)
+        loop(model, emb, steps, beams, on_prefill=lambda: mark("prefill"),
+             on_step=lambda i: mark("first") if i == 1 else None)
         mark("end")
     return marks
 
 
-def decode_bench(dev, steps):
-    """Decode rate of the 8B-style loop on the GPU (every quantized linear on
-    the HIP GEMV; attention, norms and sampling in torch)."""
-    cfg, model = decode_model(dev)
+def decode_bench(dev, steps, family="8b"):
+    """Decode rates of one decoder on the GPU, as specified and fused."""
+    spec = DECODE if family == "8b" else DECODE_1B
+    cfg, model = decode_model(dev, family)
     sync = torch.cuda.synchronize
-    run_decode(model, decode_prompt(cfg, dev, 64), 3, sync)  # loads kernels and GEMM libraries
-    marks = run_decode(model, decode_prompt(cfg, dev, DECODE["prefill"]), steps, sync)
-    decode_s = marks["end"] - marks["first"]
-    result = {
-        "workload": f"StarCoder2-8B-style decoder, {cfg.layers} layers, hidden {cfg.hidden}, "
-                    f"{cfg.heads}/{cfg.kv_heads} heads, inner {cfg.inner}, vocab {cfg.vocab}, "
-                    f"{DECODE['qtype']} weights (seeded synthetic), beam {DECODE['beams']}, prefill "
-                    f"{DECODE['prefill']} tokens (576-vector vision prompt), {steps} decode steps",
-        "steps": steps,
-        "decode_steps_per_s": round((steps - 1) / decode_s, 2),
-        "decode_ms_per_step": round(decode_s / (steps - 1) * 1e3, 3),
-        "tokens_per_s_incl_prefill": round(steps / (marks["end"] - marks["start"]), 2),
-        "prefill_ms": round((marks["prefill"] - marks["start"]) * 1e3, 1),
-        "first_step_ms": round((marks["first"] - marks["prefill"]) * 1e3, 1),
-        "weight_bytes_per_step": decoder_weight_bytes(cfg),
-    }
-    return result, model, cfg
+    out = {"workload": decode_workload(cfg, spec, family, steps), "steps": steps,
+           "weight_bytes_per_step": decoder_weight_bytes(cfg, spec)}
+    for mode in ("as_specified", "fused"):
+        as_specified = mode == "as_specified"
+        # Warm-up: loads kernels and GEMM libraries.
+        run_decode(model, decode_prompt(cfg, dev, 64, spec["prompt"]), 3, sync, spec["beams"],
+                   as_specified)
+        marks = run_decode(model, decode_prompt(cfg, dev, spec["prefill"], spec["prompt"]), steps,
+                           sync, spec["beams"], as_specified)
+        decode_s = marks["end"] - marks["first"]
+        out[mode] = {
+            "decode_steps_per_s": round((steps - 1) / decode_s, 2),
+            "decode_ms_per_step": round(decode_s / (steps - 1) * 1e3, 3),
+            "tokens_per_s_incl_prefill": round(steps / (marks["end"] - marks["start"]), 2),
+            "prefill_ms": round((marks["prefill"] - marks["start"]) * 1e3, 1),
+            "first_step_ms": round((marks["first"] - marks["prefill"]) * 1e3, 1),
+            "ops": ("reference: HIP GEMV per quantized linear; torch LayerNorm, attention, GELU, "
+                    "residual adds; whole-vocabulary torch warpers, torch.multinomial, host "
+                    "survivor selection" if as_specified else
+                    "fused: LayerNorm / GELU / residual inside the HIP GEMVs, HIP decode "
+                    "attention, HIP beam candidates and selection"),
+        }
+    model.fused = True
+    return out, model, cfg
 
 
-def decoder_weight_bytes(cfg):
-    per_layer = [(cfg.hidden + 2 * cfg.kv_heads * cfg.head_dim, cfg.hidden), (cfg.hidden, cfg.hidden),
-                 (cfg.inner, cfg.hidden), (cfg.hidden, cfg.inner)]
-    bb = BLOCK_BYTES[DECODE["qtype"]]
-    return cfg.layers * sum(n * k // 32 * bb for n, k in per_layer) + cfg.vocab * cfg.hidden // 32 * bb
+def decode_workload(cfg, spec, family, steps):
+    if family == "8b":
+        arch = (f"StarCoder2-8B-style decoder, {cfg.layers} layers, hidden {cfg.hidden}, "
+                f"{cfg.heads}/{cfg.kv_heads} heads, inner {cfg.inner}, vocab {cfg.vocab}, "
+                f"{spec['qtype']} weights")
+    else:
+        arch = (f"GPTBigCode-1B decoder, {cfg.layers} layers, hidden {cfg.hidden}, {cfg.heads} "
+                f"heads (multi-query), inner {cfg.inner}, vocab {cfg.vocab}, {spec['qtype']} "
+                f"linears, {spec['embed_qtype']} token / position tables")
+    return (f"{arch} (seeded synthetic), beam {spec['beams']}, prefill {spec['prefill']} tokens "
+            f"({spec['prompt']}-vector vision prompt), {steps} decode steps")
+
+
+def decoder_weight_bytes(cfg, spec):
+    bb = BLOCK_BYTES[spec["qtype"]]
+    if "embed_qtype" in spec:  # GPTBigCode: c_attn, attn c_proj, c_fc, mlp c_proj
+        per_layer = [(cfg.hidden + 2 * cfg.head_dim, cfg.hidden), (cfg.hidden, cfg.hidden),
+                     (cfg.inner, cfg.hidden), (cfg.hidden, cfg.inner)]
+        head_bb = BLOCK_BYTES[spec["embed_qtype"]]
+    else:
+        per_layer = [(cfg.hidden + 2 * cfg.kv_heads * cfg.head_dim, cfg.hidden),
+                     (cfg.hidden, cfg.hidden), (cfg.inner, cfg.hidden), (cfg.hidden, cfg.inner)]
+        head_bb = bb
+    return (cfg.layers * sum(n * k // 32 * bb for n, k in per_layer) +
+            cfg.vocab * cfg.hidden // 32 * head_bb)
 
 
 def decode_cpu_baseline(model, cfg, steps=2, prompt=16):
     """The same decoder on the host cores through the reference's CPU path
-    (fp32; every quantized linear as tiled dequantize + F.linear), for a
-    short prompt and a few decode steps."""
-    threads = min(os.cpu_count() or 1, 16)
+    (fp32; every quantized linear as tiled dequantize + F.linear) and the
+    reference's loop, for a short prompt and a few decode steps."""
+    threads, host_cpus = host_cores()
     torch.set_num_threads(threads)
     model.to_host()
-    emb = decode_prompt(cfg, torch.device("cpu"), prompt, torch.float32)
-    marks = run_decode(model, emb, steps, lambda: None)
+    emb = decode_prompt(cfg, torch.device("cpu"), prompt, DECODE["prompt"], torch.float32)
+    marks = run_decode(model, emb, steps, lambda: None, DECODE["beams"], as_specified=True)
     per_step = (marks["end"] - marks["prefill"]) / steps
     return {"decode_steps_per_s": round(1 / per_step, 4), "decode_ms_per_step": round(per_step * 1e3, 1),
-            "cores": threads, "kind": "port",
+            "cores": threads, "host_cpus": host_cpus, "kind": "port",
             "sample": f"{steps} beam-2 decode steps after a {prompt}-token prefill, same 32-layer "
                       f"model on the host in fp32 (reference CPU path per quantized linear)"}
 
@@ -542,6 +633,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--trials", type=int, default=5, help="timed trials of --steps steps each")
     ap.add_argument("--quick", action="store_true", help="skip the sweep and CPU baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--summarize", metavar="DIR",
@@ -551,6 +643,8 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the decode loop (for kernel traces) and print its JSON")
     ap.add_argument("--decode-steps", type=int, default=DECODE["steps"])
+    ap.add_argument("--decode-family", choices=("8b", "1b"), default="8b",
+                    help="decoder of --decode-only")
     ap.add_argument("--summarize-decode", metavar="CSV",
                     help="GEMV share of the decode steps in a kernel trace of --decode-only, then exit")
     ap.add_argument("--profile", action="store_true",
@@ -578,9 +672,11 @@ def main():
         profile_pass(dev, stream)
         return
     if args.decode_only:
-        result, _, _ = decode_bench(dev, args.decode_steps)
+        result, _, _ = decode_bench(dev, args.decode_steps, args.decode_family)
         print(json.dumps(result), flush=True)
         return
+    if args.steps < 1 or args.warmup < 0 or args.trials < 1:
+        sys.exit("--steps and --trials must be positive, --warmup not negative")
 
     # --- headline step: 8 passes over the 5 matrices, distinct copies -------
     pool = Pool(dev, q_bytes=3 * 2**30, s_bytes=2**29)
@@ -594,22 +690,26 @@ def main():
         y = torch.empty((STEP_M, n), dtype=torch.float16, device=dev)
         per_shape[name] = [make_call(xs[k], q, s, y, STEP_QTYPE, b) for q, s in cps]
         step_bytes += algorithmic_bytes(STEP_QTYPE, n, k, STEP_M, bias)
-    for i in range(COPIES):
-        for name, *_ in STEP_SHAPES:
-            calls.append(per_shape[name][i])
-    graph = capture(calls, stream)
-    warm_replays = max(1, args.warmup // COPIES)
-    time_graph(graph, stream, warm_replays)
-    replays = max(1, args.steps // COPIES)
-    steps = replays * COPIES
+    # Exactly W untimed steps, then trials of exactly K steps: step i runs the
+    # five matrices on copy i % COPIES (the warm-up's steps come first).
+    def steps_graph(first, count):
+        return capture([per_shape[name][(first + i) % COPIES]
+                        for i in range(count) for name, *_ in STEP_SHAPES], stream)
+
+    if args.warmup:
+        warm = steps_graph(0, args.warmup)
+        time_graph(warm, stream, 1)
+        del warm
+    graph = steps_graph(args.warmup, args.steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ms_replay = time_graph(graph, stream, replays)
+    trial_ms = [time_graph(graph, stream, 1) for _ in range(args.trials)]
     wall = time.perf_counter() - t0
-    ms_step = ms_replay / COPIES
+    steps = args.steps
+    ms_step = statistics.median(trial_ms) / steps
     value = step_bytes / (ms_step * 1e-3) / 1e9
     log(f"step: {ms_step * 1e3:.1f} us/step, {value:.1f} GB/s ({value / PEAK_HBM_GBS:.1%} of 8 TB/s), "
-        f"wall {wall:.3f} s for {steps} steps")
+        f"median of {args.trials} trials of {steps} steps (wall {wall:.3f} s)")
     del graph
 
     # --- dominant launch: lm_head, own graph over its 8 copies -------------
@@ -645,34 +745,47 @@ def main():
                 dequant.append(r)
                 log(f"dequant {qtype} -> {r['out']}: {r['us']:.2f} us {r['gbs']:.0f} GB/s")
 
-    cpu = None
+    cpu = cpu_rows = None
     if not args.quick and not args.no_cpu:
         log("cpu baseline ...")
         cpu = cpu_baseline()
-        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads "
+            f"({cpu['host_cpus']} host CPUs)")
+        cpu_rows = cpu_sweep()
+        log(f"cpu sweep: {len(cpu_rows['cases'])} configurations")
 
     decode = None
     if not args.quick and not args.no_decode:
-        decode, model, cfg = decode_bench(dev, args.decode_steps)
-        log(f"decode: {decode['decode_steps_per_s']} steps/s ({decode['decode_ms_per_step']} ms/step), "
-            f"{decode['tokens_per_s_incl_prefill']} tokens/s incl. prefill")
-        if not args.no_cpu:
-            decode["cpu_baseline"] = decode_cpu_baseline(model, cfg)
-            log(f"decode cpu baseline: {decode['cpu_baseline']['decode_ms_per_step']} ms/step")
-        del model
+        decode = {}
+        for family in ("1b", "8b"):
+            result, model, cfg = decode_bench(dev, args.decode_steps, family)
+            for mode in ("as_specified", "fused"):
+                r = result[mode]
+                log(f"decode {family} {mode}: {r['decode_steps_per_s']} steps/s "
+                    f"({r['decode_ms_per_step']} ms/step), {r['tokens_per_s_incl_prefill']} "
+                    f"tokens/s incl. prefill")
+            if family == "8b" and not args.no_cpu:
+                result["cpu_baseline"] = decode_cpu_baseline(model, cfg)
+                log(f"decode cpu baseline: {result['cpu_baseline']['decode_ms_per_step']} ms/step")
+            decode["starcoder2_8b" if family == "8b" else "gptbigcode_1b"] = result
+            del model
+            torch.cuda.empty_cache()
 
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": steps, "warmup": warm_replays * COPIES, "ms_per_step": round(ms_step, 5),
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded Q5_0 blocks: uniform codes, fp16 scales U[1e-3,2e-2]; fp16 x ~ N(0,1))",
         "config": {"workload": "Q5_0 GEMV sweep over the StarCoder2-8B decoder linears, batch 2 "
                                "(qkv 5632x4608, o_proj 4608x4608, c_fc 18432x4608, c_proj 4608x18432, "
                                "lm_head 49152x4608)",
                    "batch": STEP_M, "bytes_per_step": step_bytes,
-                   "frac_of_peak": round(value / PEAK_HBM_GBS, 4), "weight_copies": COPIES},
+                   "frac_of_peak": round(value / PEAK_HBM_GBS, 4), "weight_copies": COPIES,
+                   "trials": args.trials,
+                   "trial_ms_per_step": [round(t / steps, 5) for t in trial_ms]},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_sweep": cpu_rows,
         "decode": decode,
         "sweep": sweep,
         "dequant": dequant,
