@@ -430,9 +430,41 @@ int64_t split_workspace_bytes(int m, int n, int k) {
   return sl ? (int64_t)sl * m * n * 4 : 0;
 }
 
-int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t* bias,
-              void* y, int m, int n, int k, int qtype, int y_dtype, const Fusion& f,
-              void* stream, void* workspace = nullptr, int64_t workspace_bytes = 0) {
+// Scratch of svq_gemv_split_static: the K split's fp32 partial sums in a
+// file-scope device array instead of a caller's workspace. Every GPU the
+// library runs on holds its own copy at its own address until the process
+// ends. In host code `scratch` names a host-side stand-in, never the device
+// memory: its device address is resolved once per device
+// (hipGetSymbolAddress, with that device current) and only that address is
+// passed to kernels. The partial sums are written in full before they are
+// read within one call, so nothing needs clearing between calls.
+constexpr int64_t kStaticScratchBytes = SVQ_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+std::map<int, void*> g_scratch;  // device -> device address of `scratch`
+
+// The current device's address of `scratch` (0, or a positive hipError_t).
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_cache_mu);
+  auto it = g_scratch.find(dev);
+  if (it == g_scratch.end()) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress of the static scratch");
+    if (!ptr) return hip_fail(hipErrorInvalidSymbol, "static scratch has no device address");
+    it = g_scratch.emplace(dev, ptr).first;
+  }
+  *out = it->second;
+  return 0;
+}
+
+// Every argument check of a GEMV call, before any HIP call (0 or an SVQ_E*
+// code with the message set).
+int check_gemv(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t* bias,
+               void* y, int m, int n, int k, int qtype, int y_dtype, const Fusion& f,
+               void* workspace, int64_t workspace_bytes) {
   if (!valid_qtype(qtype)) return fail(SVQ_E_QTYPE, "unsupported qtype %d", qtype);
   if (m < 1 || m > SVQ_MAX_ROWS)
     return fail(SVQ_E_SHAPE, "m=%d outside 1..%d", m, SVQ_MAX_ROWS);
@@ -481,6 +513,15 @@ int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t
           return fail(SVQ_E_SHAPE, "workspace overlaps an input");
     }
   }
+  return 0;
+}
+
+int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t* bias,
+              void* y, int m, int n, int k, int qtype, int y_dtype, const Fusion& f,
+              void* stream, void* workspace = nullptr, int64_t workspace_bytes = 0) {
+  if (const int rc = check_gemv(x, q, s, bias, y, m, n, k, qtype, y_dtype, f, workspace,
+                               workspace_bytes))
+    return rc;
   const Tuning tu = tuning();
   svq::GemvArgs a{};
   a.x = static_cast<const uint16_t*>(x);
@@ -579,6 +620,31 @@ int svq_gemv_split(const void* x, const uint8_t* q, const uint16_t* s, const uin
   f.act = activation;
   return gemv_impl(x, q, s, bias, y, m, n, k, qtype, SVQ_F16, f, stream, workspace,
                    workspace_bytes);
+}
+
+int svq_gemv_split_static(const void* x, const uint8_t* q, const uint16_t* s,
+                          const uint16_t* bias, void* y, int m, int n, int k, int qtype,
+                          const uint16_t* residual, int activation, void* stream) {
+  // The checks of svq_gemv_split first (no HIP call before them), then the
+  // scratch: its size against the shape, its address on this device.
+  if (activation != SVQ_ACT_NONE && activation != SVQ_ACT_GELU_TANH)
+    return fail(SVQ_E_DTYPE, "unsupported activation %d", activation);
+  if (residual && !aligned(residual, 2)) return fail(SVQ_E_ALIGN, "misaligned residual");
+  Fusion f;
+  f.residual = residual;
+  f.act = activation;
+  if (const int rc = check_gemv(x, q, s, bias, y, m, n, k, qtype, SVQ_F16, f, nullptr, 0))
+    return rc;
+  const int64_t need = split_workspace_bytes(m, n, k);
+  if (need > kStaticScratchBytes)
+    return fail(SVQ_E_WORKSPACE,
+                "m=%d n=%d k=%d needs %lld bytes of split-K scratch; the static scratch holds "
+                "%lld (use svq_gemv_split with a workspace)",
+                m, n, k, (long long)need, (long long)kStaticScratchBytes);
+  void* ptr = nullptr;
+  if (need > 0)
+    if (const int rc = scratch_address(&ptr)) return rc;
+  return gemv_impl(x, q, s, bias, y, m, n, k, qtype, SVQ_F16, f, stream, ptr, need);
 }
 
 int svq_gemv_fused(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t* bias,

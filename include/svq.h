@@ -141,6 +141,29 @@ int svq_gemv_split(const void *x, const uint8_t *q, const uint16_t *s,
    negative SVQ_E* code for an invalid shape. */
 int64_t svq_gemv_split_workspace(int m, int n, int k, int qtype);
 
+/* Bytes of the static scratch of svq_gemv_split_static (per GPU). */
+#define SVQ_STATIC_SCRATCH_BYTES (4 << 20)
+
+/*
+ * svq_gemv_split without a workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc. It has no counterpart in the reference
+ * (whose soa_gemv, quantization.py:232-265, needs no scratch). The K split's
+ * partial sums go to a static device array of SVQ_STATIC_SCRATCH_BYTES per
+ * GPU, held until the process ends: a shape whose
+ * svq_gemv_split_workspace(m, n, k, qtype) exceeds it is rejected
+ * (SVQ_E_WORKSPACE); shapes that run in one pass use none. The call makes no
+ * hipMalloc, hipFree or other allocating call. Every call on a GPU shares
+ * that GPU's array, so calls that overlap on one GPU (streams without an
+ * order between them) race. The first call on each device resolves the
+ * array's device address (hipGetSymbolAddress, no allocation); make it
+ * before capturing a graph that records the call. Arguments, checks and
+ * results are those of svq_gemv_split.
+ */
+int svq_gemv_split_static(const void *x, const uint8_t *q, const uint16_t *s,
+                          const uint16_t *bias, void *y, int m, int n, int k, int qtype,
+                          const uint16_t *residual, int activation, void *stream);
+
 /*
  * Diagnostic with no counterpart in the reference (whose launch tuple is the
  * per-(qtype, M) table SOA_GEMV_CONFIG, quantization.py:121-127): the launch
