@@ -25,12 +25,14 @@ import numpy as np
 
 from . import _native
 
+# Tensor-name prefix of each StarVector part; a file must hold all three.
 REQUIRED_COMPONENTS = {
     "vision": "model.image_encoder.",
     "adapter": "model.image_projection.",
     "decoder": "model.svg_transformer.transformer.",
 }
-# The runtime reads the tokenizer and its EOS token; other embedded files are ignored.
+# Embedded files read back from the metadata: the tokenizer and its config
+# (the EOS token). Anything else embedded is left alone.
 EMBEDDED_TOKENIZER_FILES = ("tokenizer.json", "tokenizer_config.json")
 EMBEDDED_ASSET_PREFIX = "starvector.embedded_file."
 MAX_EMBEDDED_ASSET_BYTES = 16 * 1024 * 1024
@@ -198,7 +200,10 @@ def _decode_array(raw: bytes, elem: GGUFValueType, count: int):
 
 @dataclass(frozen=True)
 class GGUFReference:
-    """A validated StarVector GGUF: its memory-mapped tensors by name, embedded config and tokenizer files."""
+    """What `inspect_local_gguf` hands the loader: the checked file's path,
+    its tensors keyed by name (views of the file mapping), the model config
+    it carries and the tokenizer files it carries (names of the reference's
+    result type, gguf_support.py:19-26)."""
 
     path: Path
     tensor_index: dict = field(repr=False)
@@ -207,40 +212,39 @@ class GGUFReference:
 
 
 def inspect_tensor_index(tensors: Iterable) -> int:
-    """Count GGUF tensors and check every StarVector component is present."""
-    components = {key: 0 for key in REQUIRED_COMPONENTS}
-    count = 0
-    for tensor in tensors:
-        count += 1
-        for component, prefix in REQUIRED_COMPONENTS.items():
-            if tensor.name.startswith(prefix):
-                components[component] += 1
-                break
-    missing = [key for key, value in components.items() if not value]
-    if missing:
-        raise ValueError(
-            "This is not a full StarVector GGUF pack: missing tensor groups "
-            + ", ".join(missing)
-            + ". A GGUF containing only an LLM or a diffusion UNet is unsupported."
-        )
-    return count
+    """Number of tensors in the file, after checking that each StarVector part
+    (vision encoder, adapter, decoder) owns at least one of them by its name
+    prefix. The error text is the reference's (gguf_support.py:29-47)."""
+    names = [tensor.name for tensor in tensors]
+    absent = [part for part, prefix in REQUIRED_COMPONENTS.items()
+              if not any(name.startswith(prefix) for name in names)]
+    if absent:
+        raise ValueError("This is not a full StarVector GGUF pack: missing tensor groups "
+                         f"{', '.join(absent)}. A GGUF containing only an LLM or a diffusion "
+                         "UNet is unsupported.")
+    return len(names)
+
+
+def _metadata_text(reader, key):
+    """A string metadata entry's contents (str, or bytes the caller decodes),
+    or None when the file has no such key."""
+    entry = reader.get_field(key)
+    return None if entry is None else entry.contents()
 
 
 def read_embedded_config(reader) -> dict:
-    """Parse the original model config stored inside StarVector's GGUF."""
-    entry = reader.get_field("starvector.config_json")
-    if entry is None:
-        raise ValueError(
-            "This StarVector GGUF has no starvector.config_json metadata. "
-            "The model architecture cannot be constructed from this export."
-        )
-    raw = entry.contents()
-    if isinstance(raw, bytes):
-        raw = raw.decode("utf-8")
-    if not isinstance(raw, str):
+    """The model config JSON object the exporter stores under
+    starvector.config_json, parsed; the reference's errors for a missing,
+    non-string, non-JSON or non-object entry (gguf_support.py:50-67)."""
+    raw = _metadata_text(reader, "starvector.config_json")
+    if raw is None:
+        raise ValueError("This StarVector GGUF has no starvector.config_json metadata. "
+                         "The model architecture cannot be constructed from this export.")
+    text = raw.decode("utf-8") if isinstance(raw, bytes) else raw
+    if not isinstance(text, str):
         raise ValueError("starvector.config_json must be a JSON string")
     try:
-        config = json.loads(raw)
+        config = json.loads(text)
     except json.JSONDecodeError as exc:
         raise ValueError("Invalid JSON in GGUF starvector.config_json") from exc
     if not isinstance(config, dict):
@@ -249,39 +253,43 @@ def read_embedded_config(reader) -> dict:
 
 
 def read_embedded_assets(reader) -> dict[str, str]:
-    """Read required self-contained tokenizer assets directly from GGUF metadata."""
+    """The tokenizer files stored under starvector.embedded_file.<name>, as
+    text: each must be UTF-8, non-empty and at most 16 MiB, and
+    tokenizer.json must be present (the reference's checks and messages,
+    gguf_support.py:70-95)."""
     assets = {}
     for filename in EMBEDDED_TOKENIZER_FILES:
-        entry = reader.get_field(EMBEDDED_ASSET_PREFIX + filename)
-        if entry is None:
+        contents = _metadata_text(reader, EMBEDDED_ASSET_PREFIX + filename)
+        if contents is None:
             continue
-        contents = entry.contents()
         if isinstance(contents, bytes):
             try:
                 contents = contents.decode("utf-8")
             except UnicodeDecodeError as exc:
                 raise ValueError(
-                    f"Invalid StarVector GGUF: embedded {filename} is not UTF-8"
-                ) from exc
+                    f"Invalid StarVector GGUF: embedded {filename} is not UTF-8") from exc
         if not isinstance(contents, str):
             raise ValueError(f"Invalid StarVector GGUF: embedded {filename} is not a string")
-        if not contents or len(contents.encode("utf-8")) > MAX_EMBEDDED_ASSET_BYTES:
-            raise ValueError(f"Invalid StarVector GGUF: embedded {filename} is empty or too large")
+        size = len(contents.encode("utf-8"))
+        if size == 0 or size > MAX_EMBEDDED_ASSET_BYTES:
+            raise ValueError(
+                f"Invalid StarVector GGUF: embedded {filename} is empty or too large")
         assets[filename] = contents
     if "tokenizer.json" not in assets:
-        raise ValueError(
-            "Invalid StarVector GGUF: embedded tokenizer metadata is missing "
-            "(expected starvector.embedded_file.tokenizer.json)"
-        )
+        raise ValueError("Invalid StarVector GGUF: embedded tokenizer metadata is missing "
+                         "(expected starvector.embedded_file.tokenizer.json)")
     return assets
 
 
 def inspect_local_gguf(path: Path) -> GGUFReference:
+    """Open a local .gguf with this package's reader and check it is a whole
+    StarVector export: config, tokenizer, every model part, unique tensor
+    names (gguf_support.py:98-121, without the PyPI `gguf` dependency)."""
     path = Path(path).resolve(strict=True)
     if not path.is_file() or path.suffix.lower() != ".gguf":
         raise ValueError("Expected a local .gguf file")
-    # Copy-on-write mapping, as the reference opens it: torch.from_numpy gets a
-    # writable view whose writes stay in memory.
+    # Mode "c" maps the file copy-on-write: tensors built on the mapping are
+    # writable, and writes never reach the file.
     reader = GGUFReader(str(path), "c")
     config = read_embedded_config(reader)
     assets = read_embedded_assets(reader)
@@ -289,4 +297,5 @@ def inspect_local_gguf(path: Path) -> GGUFReference:
     tensor_index = {tensor.name: tensor for tensor in reader.tensors}
     if len(tensor_index) != count:
         raise ValueError("Duplicate tensor names in GGUF checkpoint")
-    return GGUFReference(path=path, tensor_index=tensor_index, model_config=config, model_assets=assets)
+    return GGUFReference(path=path, tensor_index=tensor_index, model_config=config,
+                         model_assets=assets)
