@@ -362,24 +362,34 @@ template <int QT, int M, int THREADS, int SB, int SxMul = 1, bool LN = false>
 struct XStager {
   using T = QTraits<QT>;
   static constexpr int P = T::kUnitWeights / 8;
-  const uint16_t* __restrict__ x;
+  __amdgpu_buffer_rsrc_t xr;  // the M rows of x, fp16 [M, k]
   int k, cu0, cun, stride, per_row, total;
+  float inv_row;  // 1 / per_row
   u32x4 v[SB];
   int dst[SB];
 
   __device__ __forceinline__ XStager(const uint16_t* x_, int k_, int cu0_, int cun_, int stride_)
-      : x(x_), k(k_), cu0(cu0_), cun(cun_), stride(stride_), per_row(cun_ * P),
-        total(M * cun_ * P) {}
+      : xr(make_rsrc(x_, (uint32_t)(M * k_) * 2u)), k(k_), cu0(cu0_), cun(cun_), stride(stride_),
+        per_row(cun_ * P), total(M * cun_ * P),
+        inv_row(__builtin_amdgcn_rcpf((float)(cun_ * P))) {}
+
+  // Row of piece t (0 <= t < total): t / per_row from the reciprocal. Exact
+  // for per_row <= 2^14 (x of a row fits in LDS): (t + 1/2) / per_row lies at
+  // least 2^-15 from an integer, and the product's relative error is a few
+  // 2^-24 on a quotient below 8.
+  __device__ __forceinline__ int row_of(int t) const {
+    return M == 1 ? 0 : (int)(((float)t + 0.5f) * inv_row);
+  }
 
   __device__ __forceinline__ void load_batch(int base) {
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
       int t = min(base + j * THREADS, total - 1);
-      int m = 0;
-      while (t >= per_row) { t -= per_row; ++m; }
+      const int m = row_of(t);
+      t -= m * per_row;
       const int u = t / P, pc = t - u * P;
-      v[j] = reinterpret_cast<const u32x4*>(
-          x + (size_t)m * k + (size_t)cu0 * T::kUnitWeights)[t];
+      const uint32_t off = (uint32_t)(m * k + cu0 * T::kUnitWeights) * 2u + (uint32_t)t * 16u;
+      v[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
       dst[j] = (m * P + pc) * stride + u;
     }
   }
@@ -534,10 +544,9 @@ struct XStager {
     for (int j = 0; j < SB; ++j) {
       const int t = threadIdx.x + j * THREADS;
       valid[j] = t < total;
-      int m = 0, r = valid[j] ? t : 0;
-      while (r >= per_row) { r -= per_row; ++m; }
+      const int r = valid[j] ? t : 0, m = row_of(r);
       row[j] = m;
-      col[j] = r;  // = u * P + pc: the piece's column / 8 (full rows)
+      col[j] = r - m * per_row;  // = u * P + pc: the piece's column / 8 (full rows)
     }
     float s[M], mean[M], rstd[M];
 #pragma unroll

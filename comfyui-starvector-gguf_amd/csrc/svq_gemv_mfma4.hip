@@ -69,8 +69,30 @@ size_t mfma4_lds_bytes(int qtype, int m, int k, int rows, int ksplit) {
   return stream_lds_bytes(qtype, m, k) + part;
 }
 
-hipError_t launch_gemv_mfma4(const GemvArgs& a, int qtype, int m, int rows, int groups,
+// The kernel's work plan (GemvArgs::units .. lg_ksplit) for `groups`
+// workgroups (a multiple of the K slices) of the `rows` variant.
+GemvArgs plan_mfma4(const GemvArgs& in, int qtype, int rows, int groups) {
+  GemvArgs a = in;
+  const int sl = a.partial ? a.slices : 1;
+  const int R = rows == 2 ? 2 : 1;
+  const int U = rows == 3 ? (qtype == 8 ? 2 : 3) : 1;
+  const int S = a.ksplit > 1 ? a.ksplit : 1;
+  const int P = kStreamWavesPerGroup / S;
+  const int G = groups / sl;
+  a.units = (a.k / 32) * units_per_block(qtype) / sl;
+  a.tiles = (a.n + 4 * R - 1) / (4 * R);
+  a.tile_groups = (a.tiles + P - 1) / P;
+  a.wave_major = S == 1 && a.tiles <= P * G;
+  a.tiles_hi = (a.tile_groups + G - 1) / G;
+  a.tiles_full = a.tile_groups - (a.tiles_hi - 1) * G;
+  a.steps = (a.units + 16 * U - 1) / (16 * U);
+  a.lg_ksplit = S == 4 ? 2 : S == 2 ? 1 : 0;
+  return a;
+}
+
+hipError_t launch_gemv_mfma4(const GemvArgs& in, int qtype, int m, int rows, int groups,
                              hipStream_t stream) {
+  const GemvArgs a = plan_mfma4(in, qtype, rows, groups);
   if (a.partial) {  // K slices: x staged per slice, then the slices added
     const hipError_t e = mfma4_dispatch(a, false, qtype, m, rows, groups,
                                         mfma4_lds_bytes(qtype, m, a.k / a.slices, rows, 1),

@@ -34,6 +34,17 @@ struct GemvArgs {
   // to partial[slice][m][n]; split_finish adds the slices and stores y.
   int slices;  // 2..kSplitMaxSlices with `partial`
   float* partial;
+  // Work plan of the streaming MFMA kernel, filled on the host by
+  // launch_gemv_mfma4 so that the kernel divides nothing: the grid is
+  // (K slices) x (workgroups per K slice).
+  int units;        // units of x per K slice (the whole row without slices)
+  int tiles;        // row tiles of 4 rows (8 with two row sets per lane)
+  int tile_groups;  // groups of 4 / ksplit consecutive tiles
+  int wave_major;   // at most one tile per wave, in wave-major order
+  int tiles_hi;     // tile groups of a workgroup below tiles_full; one fewer from there
+  int tiles_full;
+  int steps;        // ring steps per tile, all K ranges together
+  int lg_ksplit;    // log2 of ksplit (1, 2 or 4)
 };
 constexpr int kSplitMaxSlices = 8;
 

@@ -108,15 +108,16 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 
   const int n = a.n, k = a.k;
   const int kb = k >> 5;
-  // K slices across workgroups (a.partial set, a.slices >= 2): workgroup b
-  // takes slice b % SL of every row -- units ubase .. ubase + units, x
-  // staged for that slice only -- and writes raw partial sums. Otherwise one
-  // slice: the whole row.
-  const int SL = a.partial ? a.slices : 1;
-  const int slice = (int)blockIdx.x % SL;
-  const int units = kb * T::kUnitsPerBlock / SL;
+  // K slices across workgroups (a.partial set, gridDim.x = a.slices >= 2):
+  // workgroup (slice, b) takes that slice of every row -- units ubase ..
+  // ubase + units, x staged for that slice only -- and writes raw partial
+  // sums. Otherwise one slice: the whole row. The slices of a row set are
+  // consecutive in dispatch order.
+  const int SL = (int)gridDim.x;
+  const int slice = (int)blockIdx.x;
+  const int units = a.units;
   const int ubase = slice * units;
-  const int bx = (int)blockIdx.x / SL;  // workgroup within its slice
+  const int bx = (int)blockIdx.y;  // workgroup within its slice
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slot = lane >> 2;  // MFMA block: the unit slot of this lane
@@ -128,12 +129,12 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   // wave (p, sk) streams steps [st0, st1) of each tile of slot p. With S > 1
   // workgroup g processes tile groups g, g + G, ... (P tiles each) and the S
   // partial sums of a tile meet in LDS at the end of its group.
-  const int S = a.ksplit, P = WPG / S;
-  const int p_id = wave / S, sk = wave % S;
+  const int lg_s = a.lg_ksplit, S = 1 << lg_s, P = WPG >> lg_s;
+  const int p_id = wave >> lg_s, sk = wave & (S - 1);
   const int tile_rows = 4 * R;
-  const int tiles = (n + tile_rows - 1) / tile_rows;
-  const int groups = (tiles + P - 1) / P;
-  const int G = (int)gridDim.x / SL;
+  const int tiles = a.tiles;
+  const int groups = a.tile_groups;
+  const int G = (int)gridDim.y;
   // At most one tile per wave (S = 1): wave-major tiles (wave p of
   // workgroup g owns tile wv = p * G + g), which spreads the idle waves of a
   // short matrix over all workgroups, hence over all CUs. Otherwise workgroup
@@ -142,12 +143,14 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   // of a tile slot meet at a barrier per tile, so every wave of a workgroup
   // walks the same number of tile groups.
   const int WV = P * G;
-  const bool wave_major = S == 1 && tiles <= WV;
+  const bool wave_major = a.wave_major != 0;
   const int wv = p_id * G + bx;
+  // Tile groups bx, bx + G, ... below `groups`: tiles_hi of them for
+  // workgroups below tiles_full, one fewer from there (none past groups).
   const int my_tiles = wave_major ? (wv < tiles ? 1 : 0)
-                                  : (bx < groups ? (groups - bx + G - 1) / G : 0);
-  const int niter_all = (units + kSlots * U - 1) / (kSlots * U);
-  const int st0 = sk * niter_all / S, st1 = (sk + 1) * niter_all / S;
+                                  : (bx < a.tiles_full ? a.tiles_hi : a.tiles_hi - 1);
+  const int niter_all = a.steps;
+  const int st0 = (sk * niter_all) >> lg_s, st1 = ((sk + 1) * niter_all) >> lg_s;
   const int steps = my_tiles * (st1 - st0);
   auto tile_of = [&](int j) { return wave_major ? wv + j * WV : (bx + j * G) * P + p_id; };
   // A workgroup without tiles leaves before staging x (the same decision for
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   };
 
   uint32_t w[D][R][kWordsU];
-  uint32_t sc[D][R][U == 3 ? 2 : 1];  // U = 3: block u's scale, then u + 1 and u + 2
+  uint32_t sc[D][R][U == 3 ? 2 : 1];  // U = 3: the 8 bytes that hold blocks u .. u + 2's scales
   int pj = 0, pit = st0;
   uint32_t pqo[R], pso[R];
   row_offsets(tile_of(0), pqo, pso);
@@ -221,10 +224,14 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
         }
       }
       if constexpr (U == 3) {
-        // Three consecutive blocks (one unit each): their three scales.
-        const uint32_t soff = pso[r] + ug * 2u + oob;
-        sc[d][r][0] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff, 0, 0);
-        sc[d][r][1] = __builtin_amdgcn_raw_buffer_load_b32(sr, soff + 2u, 0, 0);
+        // Three consecutive blocks (one unit each): their three scales, the 6
+        // bytes at byte 0 or 2 of the 8 dword-aligned bytes that hold them
+        // (rows start dword-aligned: kb is even), in one load.
+        const uint32_t soff = (pso[r] + ug * 2u + oob) & ~3u;
+        const u32x2 sv =
+            __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(sr, soff, 0, 0));
+        sc[d][r][0] = sv.x;
+        sc[d][r][1] = sv.y;
       } else if constexpr (U == 2) {
         // The two halves of one Q8_0 block (u even): one scale.
         sc[d][r][0] = __builtin_amdgcn_raw_buffer_load_b16(
@@ -252,16 +259,16 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
     }
   };
 
-  // x loads first, then the weight prologue, then x is written to LDS
-  // (vector loads retire in issue order).
+  // x and bias loads first, then the weight prologue, then x is written to
+  // LDS (vector loads retire in issue order).
   XStager<QT, M, WPG * 64, kStage4Batch<QT, M>, Mfma4Traits<QT>::kSxMul, LN> st(a.x, k, ubase, units,
                                                                                units);
   st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
   st.begin(lns);
+  uint32_t bias_bits[R];  // before the prologue: waiting for it waits for x only
+  load_bias(tile_of(0), bias_bits);
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d);
-  uint32_t bias_bits[R];
-  load_bias(tile_of(0), bias_bits);
   st.finish(xs, sxs, lns);
 
   float acc[R][M];
@@ -319,9 +326,12 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
                                                            0);
               }
             }
-            // Scale of unit q: the 2-byte load, then the two halves of the 4-byte one.
+            // Scale of unit q: half q of the 8 loaded bytes, after the 2-byte
+            // lead-in when the first unit's index is odd.
             const uint32_t sbits =
-                U != 3 || q == 0 ? sc[d][r][0] : sc[d][r][1] >> (16 * (q - 1));
+                U != 3 ? sc[d][r][0]
+                       : (uint32_t)((((uint64_t)sc[d][r][1] << 32) | sc[d][r][0]) >>
+                                    (16 * q + 16 * ((ubase + U * (slot + cit * kSlots)) & 1)));
             const float scale = half_bits_to_float((uint16_t)sbits);
 #pragma unroll
             for (int m = 0; m < M; ++m)
@@ -399,8 +409,10 @@ const void* mfma4_kernel_ptr() {
 
 template <int QT, int M, int R, int D, int U, bool LN>
 hipError_t mfma4_launch(const GemvArgs& a, int groups, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((gemv_mfma4_kernel<QT, M, R, D, kStreamWavesPerGroup, U, LN>), dim3(groups),
-                     dim3(kStreamWavesPerGroup * 64), lds, stream, a);
+  // groups = K slices (gridDim.x) x workgroups per slice (gridDim.y).
+  const int sl = a.partial ? a.slices : 1;
+  hipLaunchKernelGGL((gemv_mfma4_kernel<QT, M, R, D, kStreamWavesPerGroup, U, LN>),
+                     dim3(sl, groups / sl), dim3(kStreamWavesPerGroup * 64), lds, stream, a);
   return hipGetLastError();
 }
 
