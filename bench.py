@@ -30,6 +30,7 @@ Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -41,6 +42,7 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 import __graft_entry__  # noqa: E402
@@ -402,6 +404,105 @@ def committed_traffic(name, n, k):
     return None
 
 
+TIMELINE_CASES = (  # (label, qtype, n, k, fusion)
+    ("qkv 5632x4608 + LayerNorm", "Q5_0", 5632, 4608, "ln"),
+    ("qkv 5632x4608", "Q5_0", 5632, 4608, "plain"),
+    ("o_proj 4608x4608 + residual", "Q5_0", 4608, 4608, "res"),
+    ("qkv 5632x4608 + LayerNorm", "Q4_0", 5632, 4608, "ln"),
+    ("o_proj 4608x4608 + residual", "Q4_0", 4608, 4608, "res"),
+    ("lm_head 49152x4608 + LayerNorm", "Q5_0", 49152, 4608, "ln"),
+)
+
+
+def timeline(dev, launches=10):
+    """Per-phase timeline of the streaming MFMA GEMV (M = 2) from the stamps
+    of libsvq_timeline.so, next to a coalesced plain read of the same bytes:
+    `launches` back-to-back launches (weights rotated) in one graph, stamps of
+    the fifth; launch time = first entry to last end of a launch, gap = to the
+    next launch's first entry. Phase columns: 0 / 50 / 90th percentile over the
+    busy waves, us after the launch's first entry. Prints a markdown table."""
+    lib = ctypes.CDLL(str(Path(native.__file__).resolve().parent / "libsvq_timeline.so"))
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+    lib.svq_gemv_fused.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp,
+                                   ctypes.c_float, vp, i32, vp]
+    lib.svq_gemv_fused.restype = i32
+    lib.svq_gemv.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
+    lib.svq_timeline_stamps.argtypes = [vp]
+    lib.svq_timeline_read.argtypes = [vp, ctypes.c_uint64, i32, vp, vp, vp]
+    lib.svq_last_error.restype = ctypes.c_char_p
+    stream = torch.cuda.Stream(dev)
+    m, groups_read = 2, 512
+    stamps = torch.zeros((launches, 4096 * 4 * 8), dtype=torch.int64, device=dev)
+    sink = torch.empty(4096 * 256, dtype=torch.int32, device=dev)
+    pool = Pool(dev, 1600 * 2**20, 160 * 2**20)
+
+    def run(calls):
+        g = capture(calls, stream)
+        for _ in range(3):
+            stamps.zero_()
+            torch.cuda.synchronize()
+            with torch.cuda.stream(stream):
+                g.replay()
+            stream.synchronize()
+        return stamps.cpu().numpy().reshape(launches, -1, 8)
+
+    def summary(st, phases):
+        first = [w[w[:, 0] > 0][:, 0].min() for w in st]
+        last = [w[w[:, 0] > 0][:, 4].max() for w in st]
+        dur = statistics.median((last[i] - first[i]) / 100 for i in range(1, launches - 1))
+        gap = statistics.median((first[i + 1] - last[i]) / 100 for i in range(1, launches - 1))
+        w = st[4][st[4][:, 0] > 0]
+        t0 = w[:, 0].min()
+        busy = w[w[:, 5] > 0] if phases else w
+        pct = lambda c: "/".join(f"{v:.2f}" for v in np.percentile((busy[:, c] - t0) / 100,
+                                                                   [0, 50, 90]))
+        cols = [pct(c) for c in (6, 1, 2, 3)] if phases else ["", "", "", ""]
+        return [f"{dur:.2f}", f"{gap:.2f}", *cols, pct(4)]
+
+    print("| case | qtype | launch us | gap us | x issued | x staged | step 1 | tile 1 | end |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for label, qtype, n, k, fusion in TIMELINE_CASES:
+        pool.reset()
+        cps = pool.copies(qtype, n, k, launches)
+        x = torch.randn((m, k), device=dev).half()
+        y = torch.empty((m, n), device=dev, dtype=torch.half)
+        res = torch.randn((m, n), device=dev).half()
+        lw = (torch.rand(k, device=dev) + 0.5).half()
+        lb = (torch.randn(k, device=dev) * 0.1).half()
+        code = native.QTYPE_CODE[qtype]
+
+        def gemv(i):
+            q, sc = cps[i]
+            lib.svq_timeline_stamps(stamps[i].data_ptr())
+            if fusion == "plain":
+                rc = lib.svq_gemv(x.data_ptr(), q.data_ptr(), sc.data_ptr(), None, y.data_ptr(),
+                                  m, n, k, code, 0, stream.cuda_stream)
+            else:
+                ln = fusion == "ln"
+                rc = lib.svq_gemv_fused(x.data_ptr(), q.data_ptr(), sc.data_ptr(), None,
+                                        y.data_ptr(), m, n, k, code,
+                                        lw.data_ptr() if ln else None,
+                                        lb.data_ptr() if ln else None, 1e-5,
+                                        None if ln else res.data_ptr(), 0, stream.cuda_stream)
+            lib.svq_timeline_stamps(None)
+            if rc:
+                raise RuntimeError(lib.svq_last_error().decode())
+
+        print(f"| {label} | {qtype} | " + " | ".join(summary(run([lambda i=i: gemv(i) for i in
+                                                                  range(launches)]), True)) + " |")
+        nbytes = (cps[0][0].numel() + cps[0][1].numel() * 2) // 1024 * 1024
+
+        def read(i):
+            rc = lib.svq_timeline_read(cps[i][0].data_ptr(), nbytes, groups_read, sink.data_ptr(),
+                                       stamps[i].data_ptr(), stream.cuda_stream)
+            if rc:
+                raise RuntimeError(lib.svq_last_error().decode())
+
+        print(f"| plain read, {nbytes / 1e6:.1f} MB | | " +
+              " | ".join(summary(run([lambda i=i: read(i) for i in range(launches)]), False)) + " |")
+        sys.stdout.flush()
+
+
 def host_cores():
     """(threads the CPU baselines use, the host's CPU count): every CPU this
     process may run on (its affinity mask, which on a GPU box is the share
@@ -647,6 +748,8 @@ def main():
                     help="decoder of --decode-only")
     ap.add_argument("--summarize-decode", metavar="CSV",
                     help="GEMV share of the decode steps in a kernel trace of --decode-only, then exit")
+    ap.add_argument("--timeline", action="store_true",
+                    help="per-phase timeline of the GEMV (libsvq_timeline.so); prints a table")
     ap.add_argument("--profile", action="store_true",
                     help="eager launches for rocprofv3: every step GEMV on 8 copies, twice, then "
                          "16 torch copies of 256 MiB (the known-size copy that scales FETCH_SIZE "
@@ -670,6 +773,9 @@ def main():
     log(f"device: {torch.cuda.get_device_name(dev)}")
     if args.profile:
         profile_pass(dev, stream)
+        return
+    if args.timeline:
+        timeline(dev)
         return
     if args.decode_only:
         result, _, _ = decode_bench(dev, args.decode_steps, args.decode_family)

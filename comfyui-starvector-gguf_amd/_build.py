@@ -69,5 +69,41 @@ def build_library(jobs: int | None = None) -> Path:
     return LIB_PATH
 
 
+# The timeline build (libsvq_timeline.so): the units holding the streaming
+# MFMA kernel and the C ABI recompiled with SVQ_TIMELINE, linked with the other
+# objects of the product build. The kernel then writes per-wave phase stamps
+# when svq_timeline_stamps has set a buffer; libsvq.so carries no stamp code.
+TIMELINE_LIB = PKG_DIR / "libsvq_timeline.so"
+TIMELINE_OBJ_DIR = PKG_DIR / "_obj_timeline"
+TIMELINE_UNITS = ("svq_api", "svq_gemv_mfma4", "svq_gemv_mfma4_wide")
+
+
+def _compile_timeline(src: Path) -> Path:
+    obj = TIMELINE_OBJ_DIR / (src.stem + ".o")
+    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-DSVQ_TIMELINE=1", "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc (timeline) failed for {src.name}:\n{proc.stderr}")
+    return obj
+
+
+def build_timeline_library(jobs: int | None = None) -> Path:
+    """Link libsvq_timeline.so (after build_library, whose objects it reuses)."""
+    TIMELINE_OBJ_DIR.mkdir(exist_ok=True)
+    units = [CSRC / f"{u}.hip" for u in TIMELINE_UNITS]
+    with ThreadPoolExecutor(max_workers=jobs or len(units)) as pool:
+        objects = list(pool.map(_compile_timeline, units))
+    objects += [o for o in sorted(OBJ_DIR.glob("*.o")) if o.stem not in TIMELINE_UNITS]
+    tmp = TIMELINE_LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", "-o", str(tmp),
+           *map(str, objects)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link of libsvq_timeline.so failed:\n{proc.stderr}")
+    os.replace(tmp, TIMELINE_LIB)
+    return TIMELINE_LIB
+
+
 if __name__ == "__main__":
     print(build_library())
+    print(build_timeline_library())

@@ -14,7 +14,18 @@
 #include "../../include/svq.h"
 #include "svq_launch.h"
 
+#if SVQ_TIMELINE
+namespace svq {
+hipError_t launch_timeline_read(const void* p, uint32_t bytes, int groups, uint32_t* sink,
+                                unsigned long long* stamps, hipStream_t stream);
+}
+#endif
+
 namespace {
+
+#if SVQ_TIMELINE
+unsigned long long* g_stamps = nullptr;  // svq_timeline_stamps
+#endif
 
 thread_local char g_error[256] = "";
 
@@ -524,6 +535,9 @@ int gemv_impl(const void* x, const uint8_t* q, const uint16_t* s, const uint16_t
     return rc;
   const Tuning tu = tuning();
   svq::GemvArgs a{};
+#if SVQ_TIMELINE
+  a.stamps = g_stamps;
+#endif
   a.x = static_cast<const uint16_t*>(x);
   a.q = q;
   a.s = s;
@@ -590,6 +604,22 @@ int set_error(int code, const char* msg) { return fail(code, "%s", msg); }
 extern "C" {
 
 int svq_abi_version(void) { return SVQ_ABI_VERSION; }
+
+#if SVQ_TIMELINE
+void svq_timeline_stamps(void* stamps) { g_stamps = static_cast<unsigned long long*>(stamps); }
+
+int svq_timeline_read(const void* p, uint64_t bytes, int groups, void* sink, void* stamps,
+                      void* stream) {
+  if (!p || !sink || !stamps || bytes % 1024 || bytes >= (1ull << 31) || groups < 1 ||
+      groups > 4096)
+    return fail(SVQ_E_SHAPE, "invalid timeline read");
+  const hipError_t e =
+      svq::launch_timeline_read(p, (uint32_t)bytes, groups, static_cast<uint32_t*>(sink),
+                                static_cast<unsigned long long*>(stamps),
+                                static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? 0 : hip_fail(e, "timeline read launch");
+}
+#endif
 
 const char* svq_last_error(void) { return g_error; }
 

@@ -110,4 +110,45 @@ hipError_t launch_gemv_mfma4(const GemvArgs& in, int qtype, int m, int rows, int
                         stream, nullptr);
 }
 
+#if SVQ_TIMELINE
+namespace {
+// A plain coalesced read of `bytes` (a multiple of 16): wave w of the grid
+// reads the 1 KB pieces w, w + W, ... (64 lanes x 16 bytes each) and stamps
+// its entry and end like the GEMV (slots 0 and 4).
+__global__ __launch_bounds__(256) void timeline_read_kernel(const uint8_t* p, uint32_t bytes,
+                                                            uint32_t* sink,
+                                                            unsigned long long* stamps) {
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(p, bytes);
+  const uint32_t waves = gridDim.x * 4u, wave = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u, pieces = bytes / 1024u;
+  uint32_t acc = 0;
+  for (uint32_t i = wave; i < pieces; i += 8u * waves) {
+    u32x4 v[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) {
+      const uint32_t pc = i + j * waves;
+      v[j] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, pc < pieces ? pc * 1024u + lane * 16u
+                                                                       : kOutOfRange, 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
+  sink[blockIdx.x * 256u + threadIdx.x] = acc;
+  if (lane == 0) {
+    stamps[wave * kTimelineSlots] = t0;
+    stamps[wave * kTimelineSlots + 4] = __builtin_amdgcn_s_memrealtime();
+  }
+}
+}  // namespace
+
+hipError_t launch_timeline_read(const void* p, uint32_t bytes, int groups, uint32_t* sink,
+                                unsigned long long* stamps, hipStream_t stream) {
+  hipLaunchKernelGGL(timeline_read_kernel, dim3(groups), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(p), bytes, sink, stamps);
+  return hipGetLastError();
+}
+#endif
+
 }  // namespace svq

@@ -45,7 +45,15 @@ struct GemvArgs {
   int tiles_full;
   int steps;        // ring steps per tile, all K ranges together
   int lg_ksplit;    // log2 of ksplit (1, 2 or 4)
+  // Per-wave phase stamps of the streaming MFMA kernel, written only by
+  // libsvq_timeline.so (built with SVQ_TIMELINE); null otherwise.
+  unsigned long long* stamps;
 };
+
+// Timeline builds: stamp slots per wave, [linear workgroup * 4 + wave][8]:
+// 0 entry, 1 x staged, 2 first step done, 3 first tile summed, 4 end,
+// 5 tiles of the wave, 6 x loads issued, 7 work split known.
+constexpr int kTimelineSlots = 8;
 constexpr int kSplitMaxSlices = 8;
 
 struct GemvShape {

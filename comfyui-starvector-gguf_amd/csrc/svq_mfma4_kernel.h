@@ -46,6 +46,19 @@ typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kOutOfRange = 0x80000000u;  // past every buffer range (< 2^31 bytes)
+
+// Phase stamps (100 MHz real-time clock) of lane 0 of every wave, in builds
+// with SVQ_TIMELINE only (libsvq_timeline.so); nothing otherwise.
+#if SVQ_TIMELINE
+#define SVQ_STAMP(slot, value)                                    \
+  do {                                                            \
+    if (stamps_ && (threadIdx.x & 63) == 0) stamps_[slot] = (value); \
+  } while (0)
+#else
+#define SVQ_STAMP(slot, value) \
+  do {                         \
+  } while (0)
+#endif
 constexpr int kSlots = 16;                     // unit slots per row: MFMA blocks per wave
 
 // Output and offset scaling: Q4_0 and Q5_0 codes are placed as 16 * code.
@@ -106,6 +119,13 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   extern __shared__ u32x4 lds[];
   __shared__ u32x2 q5_table[QT == 5 ? 256 : 1];
 
+#if SVQ_TIMELINE
+  const unsigned long long t_entry = __builtin_amdgcn_s_memrealtime();
+  unsigned long long* stamps_ =
+      a.stamps ? a.stamps + ((blockIdx.y * gridDim.x + blockIdx.x) * WPG + (threadIdx.x >> 6)) *
+                                kTimelineSlots
+               : nullptr;
+#endif
   const int n = a.n, k = a.k;
   const int kb = k >> 5;
   // K slices across workgroups (a.partial set, gridDim.x = a.slices >= 2):
@@ -156,6 +176,11 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   // A workgroup without tiles leaves before staging x (the same decision for
   // all its waves): wave-major, when its first wave (wv = g) has none;
   // otherwise when it has no tile group.
+#if SVQ_TIMELINE
+  SVQ_STAMP(0, t_entry);
+  SVQ_STAMP(5, 0ull);
+  SVQ_STAMP(7, __builtin_amdgcn_s_memrealtime());
+#endif
   if (bx >= (wave_major ? tiles : groups)) return;
   const uint32_t row_bytes = (uint32_t)kb * T::kBlockQ;
 
@@ -265,11 +290,14 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
                                                                                units);
   st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
   st.begin(lns);
+  SVQ_STAMP(6, __builtin_amdgcn_s_memrealtime());
   uint32_t bias_bits[R];  // before the prologue: waiting for it waits for x only
   load_bias(tile_of(0), bias_bits);
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d);
   st.finish(xs, sxs, lns);
+  SVQ_STAMP(1, __builtin_amdgcn_s_memrealtime());
+  SVQ_STAMP(5, (unsigned long long)my_tiles);
 
   float acc[R][M];
 #pragma unroll
@@ -340,6 +368,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
         }
       }
       issue(d);  // refill with the step D ahead (out of range past the end)
+      if (s == 0 && d == 0) SVQ_STAMP(2, __builtin_amdgcn_s_memrealtime());
       if (s + d < steps && ++cit == st1) {
         // Tile done: add the 16 unit slots of each row (and the S K-ranges),
         // store, next tile.
@@ -348,6 +377,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int m = 0; m < M; ++m) acc[r][m] = slot_sum(acc[r][m]);
+        if (cj == 0) SVQ_STAMP(3, __builtin_amdgcn_s_memrealtime());
         if (S > 1) {
           float* buf = part + (cj & 1) * WPG * R * M * 4;
           if (slot == 0) {
@@ -400,6 +430,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
       }
     }
   }
+  SVQ_STAMP(4, __builtin_amdgcn_s_memrealtime());
 }
 
 template <int QT, int M, int R, int D, int U, bool LN>

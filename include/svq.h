@@ -365,6 +365,27 @@ const void *svq_gguf_tensor_data(const svq_gguf *g, int64_t i); /* NULL if out o
 int svq_pack_soa(const uint8_t *aos, int64_t nblocks, int qtype, uint8_t *q, uint8_t *s,
                  int threads);
 
+/*
+ * Phase timeline of the streaming GEMV (libsvq_timeline.so only: the same
+ * sources built with SVQ_TIMELINE; libsvq.so exports neither function). No
+ * counterpart in the reference: profiling support for this library.
+ *
+ * svq_timeline_stamps: GEMV calls made after it (from any thread) write, for
+ * every wave of the streaming MFMA kernel, 8 uint64 stamps of the 100 MHz
+ * real-time clock to stamps[(linear workgroup * 4 + wave) * 8 ..]: entry,
+ * x staged, first step done, first tile summed, end, the wave's tile count
+ * (a count, not a time), x loads issued, work split known. The buffer must
+ * hold 32 uint64 per workgroup of the launch; NULL stops stamping.
+ *
+ * svq_timeline_read: a plain coalesced read of `bytes` (a multiple of 1024,
+ * below 2^31) at p by `groups` workgroups of 4 waves, stamping entry and end
+ * (stamps 0 and 4 of each wave) the same way; sink receives 256 uint32 per
+ * workgroup.
+ */
+void svq_timeline_stamps(void *stamps);
+int svq_timeline_read(const void *p, uint64_t bytes, int groups, void *sink, void *stamps,
+                      void *stream);
+
 #ifdef __cplusplus
 }
 #endif

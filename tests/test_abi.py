@@ -28,11 +28,41 @@ def test_header_declares_the_entry_points():
             "svq_decode_attention_workspace"} <= set(names)
 
 
+TIMELINE_ONLY = {"svq_timeline_stamps", "svq_timeline_read"}
+TIMELINE_LIB = Path(native.__file__).resolve().parent / "libsvq_timeline.so"
+
+
 def test_library_exports_every_declared_function():
     lib = native.load()
     for name in declared_functions():
+        if name in TIMELINE_ONLY:
+            continue
         assert hasattr(lib, name), name
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
+
+
+def test_timeline_library_exports_everything_and_libsvq_no_timeline():
+    """libsvq_timeline.so (the SVQ_TIMELINE build) exports every declared
+    function; libsvq.so carries no timeline entry point."""
+    names = declared_functions()
+    assert TIMELINE_ONLY <= set(names)
+    timeline = ctypes.CDLL(str(TIMELINE_LIB))
+    for name in names:
+        assert hasattr(timeline, name), name
+    lib = native.load()
+    for name in TIMELINE_ONLY:
+        assert not hasattr(lib, name), name
+
+
+def test_timeline_read_rejects_bad_arguments():
+    timeline = ctypes.CDLL(str(TIMELINE_LIB))
+    f = timeline.svq_timeline_read
+    f.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_void_p,
+                  ctypes.c_void_p, ctypes.c_void_p]
+    assert f(X, 1000, 512, Y, B, None) == -2  # not a multiple of 1024
+    assert f(X, 1 << 31, 512, Y, B, None) == -2  # too large
+    assert f(X, 1024, 0, Y, B, None) == -2  # no workgroups
+    assert f(None, 1024, 512, Y, B, None) == -2
 
 
 def test_abi_version():
