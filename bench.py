@@ -411,6 +411,9 @@ TIMELINE_CASES = (  # (label, qtype, n, k, fusion)
     ("qkv 5632x4608 + LayerNorm", "Q4_0", 5632, 4608, "ln"),
     ("o_proj 4608x4608 + residual", "Q4_0", 4608, 4608, "res"),
     ("lm_head 49152x4608 + LayerNorm", "Q5_0", 49152, 4608, "ln"),
+    ("lm_head 49152x4608", "Q5_0", 49152, 4608, "plain"),
+    ("c_fc 18432x4608", "Q5_0", 18432, 4608, "plain"),
+    ("lm_head 49152x4608", "Q4_0", 49152, 4608, "plain"),
 )
 
 

@@ -291,7 +291,14 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   // 22.6 us, lm_head 46.5 -> 40.2 us at M = 5) and for Q8_0 at M = 8
   // (lm_head 85.5 -> 65.1 us); Q8_0 keeps whole-block lanes at M = 5..7.
   const bool q4_rows3 = m == 2 || (m >= 3 && q_bytes <= (64ull << 20));
-  const bool rows3 = m <= 4 ? qtype != SVQ_Q4_0 || q4_rows3 : qtype == SVQ_Q8_0 && m < 8;
+  // Q8_0 rows of 2048 weights or fewer at M <= 2 take two row sets of
+  // one-unit lanes, whose loads cover whole cache lines (non-temporal):
+  // 8192 x 2048 at M = 1 7.0 -> 6.3 us, M = 2 7.1 -> 6.6 us; 49152 x 2048 at
+  // M = 2 21.2 -> 20.5 us. At K = 4608 whole-block lanes stay faster.
+  const bool q8_short = qtype == SVQ_Q8_0 && m <= 2 && k <= 2048;
+  const bool rows3 = q8_short ? false
+                     : m <= 4 ? qtype != SVQ_Q4_0 || q4_rows3
+                              : qtype == SVQ_Q8_0 && m < 8;
   int rows = tu.mfma_r ? tu.mfma_r : (rows3 && multi ? 3 : 2);
   if (rows == 3 && !multi) rows = 2;
   int wmax = 0, tiles = 0;

@@ -287,12 +287,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
                                            (int)bytes, 0x00020000);
 }
 
-// Load one unit's dwords at byte offset `off` of a buffer resource.
-template <int QT>
+// Cache policy of weight loads that stream whole 16-byte units: the
+// non-temporal hint (the `nt` bit of the buffer load's cache-policy operand).
+// Measured on row-contiguous 16-byte unit loads (Q4_0, Q8_0), whose every
+// load instruction covers whole cache lines: 49152 x 4608 at M = 1, Q4_0
+// 27.2 -> 24.5 us and Q8_0 46.0 -> 41.4 us. Loads that cover a line in
+// parts across instructions (the 20-byte Q5_0 units, runs of blocks per
+// lane) turn 1.3-1.7x slower with it, so those keep the default policy.
+constexpr int kLoadNonTemporal = 2;
+
+// Load one unit's dwords at byte offset `off` of a buffer resource, with
+// cache policy AUX for the 16-byte part.
+template <int QT, int AUX = 0>
 __device__ __forceinline__ void load_unit_buf(__amdgpu_buffer_rsrc_t r,
                                               uint32_t off,
                                               uint32_t (&w)[QTraits<QT>::kWords]) {
-  const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
   w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
   if constexpr (QT == 5) w[4] = __builtin_amdgcn_raw_buffer_load_b32(r, off + 16, 0, 0);
 }

@@ -116,7 +116,9 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
     const uint32_t oob = (uint32_t)(!valid) * kOutOfRange;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      load_unit_buf<QT>(qr, pqo[r] + (uint32_t)u * T::kUnitBytes + oob, w[d][r]);
+      // Lanes of a row read consecutive units: whole cache lines per load.
+      load_unit_buf<QT, QT == 5 ? 0 : kLoadNonTemporal>(
+          qr, pqo[r] + (uint32_t)u * T::kUnitBytes + oob, w[d][r]);
       sc[d][r] = __builtin_amdgcn_raw_buffer_load_b16(
           sr, pso[r] + (uint32_t)(u / T::kUnitsPerBlock) * 2u + oob, 0, 0);
     }

@@ -262,7 +262,9 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
         sc[d][r][0] = __builtin_amdgcn_raw_buffer_load_b16(
             sr, pso[r] + (ug / 2u) * 2u + oob, 0, 0);
       } else {
-        load_unit_buf<QT>(qr, pqo[r] + ug * T::kUnitBytes + oob, w[d][r]);
+        // 16 lanes of a row read 16 consecutive units: whole cache lines.
+        load_unit_buf<QT, QT == 5 ? 0 : kLoadNonTemporal>(qr, pqo[r] + ug * T::kUnitBytes + oob,
+                                                          w[d][r]);
         sc[d][r][0] = __builtin_amdgcn_raw_buffer_load_b16(
             sr, pso[r] + (ug / T::kUnitsPerBlock) * 2u + oob, 0, 0);
       }
