@@ -423,7 +423,10 @@ def timeline(dev, launches=10):
     `launches` back-to-back launches (weights rotated) in one graph, stamps of
     the fifth; launch time = first entry to last end of a launch, gap = to the
     next launch's first entry. Phase columns: 0 / 50 / 90th percentile over the
-    busy waves, us after the launch's first entry. Prints a markdown table."""
+    busy waves, us after the launch's first entry; the last column is the
+    median end of the waves of the first and of the second half of the
+    workgroups (with two workgroups per CU, the first half holds one per CU).
+    Prints a markdown table."""
     lib = ctypes.CDLL(str(Path(native.__file__).resolve().parent / "libsvq_timeline.so"))
     vp, i32 = ctypes.c_void_p, ctypes.c_int
     lib.svq_gemv_fused.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp,
@@ -460,10 +463,15 @@ def timeline(dev, launches=10):
         pct = lambda c: "/".join(f"{v:.2f}" for v in np.percentile((busy[:, c] - t0) / 100,
                                                                    [0, 50, 90]))
         cols = [pct(c) for c in (6, 1, 2, 3)] if phases else ["", "", "", ""]
-        return [f"{dur:.2f}", f"{gap:.2f}", *cols, pct(4)]
+        ends = (st[4][:, 4] - t0) / 100
+        live = st[4][:, 0] > 0
+        half = np.arange(len(ends)) // 4 < live.sum() // 8  # workgroups of 4 waves
+        split = "/".join(f"{np.median(ends[live & sel]):.2f}" for sel in (half, ~half))
+        return [f"{dur:.2f}", f"{gap:.2f}", *cols, pct(4), split]
 
-    print("| case | qtype | launch us | gap us | x issued | x staged | step 1 | tile 1 | end |")
-    print("|---|---|---|---|---|---|---|---|---|")
+    print("| case | qtype | launch us | gap us | x issued | x staged | step 1 | tile 1 | end | "
+          "end by half |")
+    print("|---|---|---|---|---|---|---|---|---|---|")
     for label, qtype, n, k, fusion in TIMELINE_CASES:
         pool.reset()
         cps = pool.copies(qtype, n, k, launches)

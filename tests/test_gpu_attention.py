@@ -178,6 +178,23 @@ def test_decode_attention_consecutive_calls_share_workspace(cuda_device):
         assert (out - ref).abs().max().item() <= 2e-3 * ref.abs().max().item()
 
 
+def test_decode_attention_shapes_share_workspace(cuda_device):
+    """Calls of different shapes (rows, heads, kv heads, span) on one
+    workspace, each seeing only its own partial results."""
+    ws = native.attention_workspace(cuda_device, 4, 36, 4, 1537)
+    for rows, heads, kvh, cap, span, pos, seed in ((4, 36, 4, 1600, 1537, 900, 11),
+                                                   (1, 16, 1, 300, 64, 63, 12),
+                                                   (2, 32, 2, 700, 700, 650, 13),
+                                                   (3, 36, 4, 200, 129, 128, 14)):
+        print(f"attention shapes share workspace rows={rows} heads={heads} kvh={kvh} span={span}",
+              flush=True)
+        case = make_case(rows, heads, kvh, cap, span, pos, seed=seed)
+        keys, values, out = run_kernel(case, cuda_device, workspace=ws)
+        _, _, ref = reference(case)
+        assert torch.isfinite(out).all()
+        assert (out - ref).abs().max().item() <= 2e-3 * ref.abs().max().item()
+
+
 def test_decode_attention_graph_replays(cuda_device):
     """Captured once, replayed with the position advanced between replays
     (eager work and synchronization in between): each replay writes the new
