@@ -256,6 +256,14 @@ def _short_kernel(name):
     return name
 
 
+def _grid(r):
+    """Launch shape of a trace row: total threads, and slices x workgroups when 2-D."""
+    x, y, z = (int(r[f"Grid_Size_{a}"]) for a in "XYZ")
+    if y == 1 and z == 1:
+        return str(x)
+    return f"{x * y * z} ({x // int(r['Workgroup_Size_X'])}x{y * z} wg)"
+
+
 def _read_csv(path):
     import csv
     with open(path, newline="") as f:
@@ -314,13 +322,13 @@ def summarize(root: Path):
                 if "_finish" in mine[0]:
                     kname += " + split_finish_kernel"
                 out.append(f"| {name} {n}x{k} | {kname} | "
-                           f"{mine[0]['Grid_Size_X']} | {mine[0]['VGPR_Count']} | "
+                           f"{_grid(mine[0])} | {mine[0]['VGPR_Count']} | "
                            f"{mine[0]['LDS_Block_Size']} | {len(mine)} | {avg:.2f} | {min(durs):.2f} | "
                            f"{nbytes / avg / 1e3:.0f} | {nbytes / avg / 1e3 / PEAK_HBM_GBS:.1%} |")
         else:
             groups = {}
             for r in gemv:
-                key = (_short_kernel(r["Kernel_Name"]), r["Grid_Size_X"], r["LDS_Block_Size"])
+                key = (_short_kernel(r["Kernel_Name"]), _grid(r), r["LDS_Block_Size"])
                 groups.setdefault(key, []).append(r)
             out.append("| kernel | grid | LDS B | dispatches | avg us | min us | max us |")
             out.append("|---|---|---|---|---|---|---|")
@@ -330,7 +338,7 @@ def summarize(root: Path):
                            f"{min(durs):.2f} | {max(durs):.2f} |")
         if copies and len(gemv) == profile_dispatches:
             durs = _durations_us(copies)
-            out.append(f"| torch copy 256 MiB | {copies[0]['Grid_Size_X']} | | {len(copies)} | "
+            out.append(f"| torch copy 256 MiB | {_grid(copies[0])} | | {len(copies)} | "
                        f"{sum(durs) / len(durs):.2f} | {min(durs):.2f} | "
                        f"{2 * 2**28 / (sum(durs) / len(durs)) / 1e3:.0f} GB/s read+write |")
         out.append("")
@@ -730,13 +738,14 @@ def summarize_decode(trace: Path):
     by = {}
     for d, r in zip(durs, phase):
         key = _short_kernel(r["Kernel_Name"])[:70]
-        by[key] = by.get(key, 0.0) + d
+        t, n = by.get(key, (0.0, 0))
+        by[key] = (t + d, n + 1)
     span = (int(phase[-1]["End_Timestamp"]) - int(phase[0]["Start_Timestamp"])) / 1e3
     out = [f"decode phase: {len(phase)} dispatches, kernel time {total:.0f} us, span {span:.0f} us",
            f"GEMV kernels: {gemv:.0f} us = {gemv / total:.1%} of kernel time, {gemv / span:.1%} of the span",
-           "| kernel | total us | share |", "|---|---|---|"]
-    for key, d in sorted(by.items(), key=lambda kv: -kv[1])[:15]:
-        out.append(f"| {key} | {d:.0f} | {d / total:.1%} |")
+           "| kernel | calls | avg us | total us | share |", "|---|---|---|---|---|"]
+    for key, (d, n) in sorted(by.items(), key=lambda kv: -kv[1][0])[:15]:
+        out.append(f"| {key} | {n} | {d / n:.2f} | {d:.0f} | {d / total:.1%} |")
     print("\n".join(out))
 
 

@@ -19,16 +19,21 @@ COPY = "__amd_rocclr_copyBuffer"
 
 
 def write_trace(path, names):
-    """Dispatches of 10 us each, 1 us apart, in the order given."""
+    """Dispatches of 10 us each, 1 us apart, in the order given. An entry is a
+    kernel name (launched as 1 slice x 512 workgroups of 256 threads) or a
+    (name, slices, workgroups per slice) tuple."""
     with open(path, "w", newline="") as f:
         w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Start_Timestamp",
-                                          "End_Timestamp", "Grid_Size_X", "VGPR_Count",
+                                          "End_Timestamp", "Workgroup_Size_X", "Grid_Size_X",
+                                          "Grid_Size_Y", "Grid_Size_Z", "VGPR_Count",
                                           "LDS_Block_Size"])
         w.writeheader()
-        for i, name in enumerate(names):
+        for i, entry in enumerate(names):
+            name, slices, groups = entry if isinstance(entry, tuple) else (entry, 1, 512)
             w.writerow(dict(Dispatch_Id=i + 1, Kernel_Name=name, Start_Timestamp=i * 11000,
-                            End_Timestamp=i * 11000 + 10000, Grid_Size_X=131072, VGPR_Count=56,
-                            LDS_Block_Size=2048))
+                            End_Timestamp=i * 11000 + 10000, Workgroup_Size_X=256,
+                            Grid_Size_X=256 * slices, Grid_Size_Y=groups, Grid_Size_Z=1,
+                            VGPR_Count=56, LDS_Block_Size=2048))
 
 
 def profile_order():
@@ -37,9 +42,10 @@ def profile_order():
     names = []
     for _ in range(2 * bench.COPIES):
         for name, *_ in bench.STEP_SHAPES:
-            names.append(GEMV)
             if name == "c_proj":
-                names.append(FINISH)
+                names += [(GEMV, 4, 128), (FINISH, 18, 1)]
+            else:
+                names.append(GEMV)
     return names + [COPY] * 16
 
 
@@ -51,6 +57,8 @@ def test_profile_trace_maps_split_gemv_to_its_shape(tmp_path, capsys):
     assert "split_finish_kernel" in lines["| c_proj 4608x18432"]
     assert " 20.00 " in lines["| c_proj 4608x18432"]   # both kernels: 10 + 10 us
     assert " 10.00 " in lines["| qkv 5632x4608"]
+    assert " 131072 (4x128 wg) " in lines["| c_proj 4608x18432"]   # 2-D launch: K slices x groups
+    assert " 131072 (1x512 wg) " in lines["| qkv 5632x4608"]
     assert f"({2 * bench.COPIES * len(bench.STEP_SHAPES)} GEMV dispatches)" in out
 
 
