@@ -283,20 +283,32 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   const bool multi = qtype == SVQ_Q8_0 || units % 48 == 0;
   const int unit_run = qtype == SVQ_Q8_0 ? 2 : 3;
   // Defaults: variant 3 for Q5_0 and Q8_0 (measured 2-9% faster than two row
-  // sets at K = 4608 and 18432). Q4_0 takes it from M = 2 (8B beam-2 decode
-  // 468 -> 479 steps/s; at M = 3..4 c_fc 16.1 -> 14.6 us and c_proj's slices
-  // 18.1 -> 16.9 us), except matrices over 64 MiB at M = 3..4 (lm_head 27.7
-  // against 28.5 us), and keeps two row sets, which share each x read, at M =
-  // 1. With two A halves (M >= 5) two row sets win for Q5_0 (c_fc 24.2 ->
-  // 22.6 us, lm_head 46.5 -> 40.2 us at M = 5) and for Q8_0 at M = 8
-  // (lm_head 85.5 -> 65.1 us); Q8_0 keeps whole-block lanes at M = 5..7.
-  const bool q4_rows3 = m == 2 || (m >= 3 && q_bytes <= (64ull << 20));
+  // sets at K = 4608 and 18432). Q4_0 takes it at M = 2..4 for matrices up
+  // to 64 MiB (8B beam-2 decode 468 -> 479 steps/s; qkv 5632 x 4608 at M = 2
+  // 7.7 against 8.1 us; at M = 3..4 c_fc 16.1 -> 14.6 us and c_proj's slices
+  // 18.1 -> 16.9 us). Larger Q4_0 matrices read one unit per lane in two row
+  // sets, whose loads cover whole cache lines with the non-temporal hint
+  // (lm_head 49152 x 4608 at M = 2: 26.6 -> 24.0 us back to back, 27.2 ->
+  // 26.3 us inside the decode step). In back-to-back launches one-unit lanes
+  // also win on c_fc and c_proj's slices at M = 2 (13.5 -> 13.0 and 16.1 ->
+  // 15.4 us), but inside the decode step, behind the kernels that write
+  // their x, they lose (15.1 -> 16.6 and 13.1 -> 13.8 us). M = 1 keeps two
+  // row sets, which share each x read. With two A halves (M >= 5) two row
+  // sets win for Q5_0 (c_fc 24.2 -> 22.6 us, lm_head 46.5 -> 40.2 us at M =
+  // 5) and for Q8_0 at M = 8 (lm_head 85.5 -> 65.1 us); Q8_0 keeps
+  // whole-block lanes at M = 5..7.
+  const bool q4_rows3 = m >= 2 && m <= 4 && q_bytes <= (64ull << 20);
   // Q8_0 rows of 2048 weights or fewer at M <= 2 take two row sets of
-  // one-unit lanes, whose loads cover whole cache lines (non-temporal):
-  // 8192 x 2048 at M = 1 7.0 -> 6.3 us, M = 2 7.1 -> 6.6 us; 49152 x 2048 at
-  // M = 2 21.2 -> 20.5 us. At K = 4608 whole-block lanes stay faster.
-  const bool q8_short = qtype == SVQ_Q8_0 && m <= 2 && k <= 2048;
-  const bool rows3 = q8_short ? false
+  // one-unit lanes, whose loads cover whole cache lines (non-temporal), on
+  // matrices of more than 4096 rows: 8192 x 2048 at M = 1 7.0 -> 6.3 us, M =
+  // 2 7.1 -> 6.6 us; 49152 x 2048 at M = 2 21.2 -> 20.5 us. Fewer rows keep
+  // whole-block lanes (2304 x 2048 at M = 2: 4.6 against 5.9 us). At K =
+  // 4608 whole-block lanes stay faster, except on matrices over 128 MiB at M
+  // = 2..4, where enough row tiles remain to balance two row sets (lm_head
+  // 49152 x 4608: 45.1 -> 42.1 us at M = 2, 47.5 -> 43.9 us at M = 4).
+  const bool q8_short = qtype == SVQ_Q8_0 && m <= 2 && k <= 2048 && n > 4096;
+  const bool q8_large = qtype == SVQ_Q8_0 && m >= 2 && m <= 4 && q_bytes > (128ull << 20);
+  const bool rows3 = q8_short || q8_large ? false
                      : m <= 4 ? qtype != SVQ_Q4_0 || q4_rows3
                               : qtype == SVQ_Q8_0 && m < 8;
   int rows = tu.mfma_r ? tu.mfma_r : (rows3 && multi ? 3 : 2);
