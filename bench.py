@@ -431,7 +431,8 @@ def timeline(dev, launches=10):
     `launches` back-to-back launches (weights rotated) in one graph, stamps of
     the fifth; launch time = first entry to last end of a launch, gap = to the
     next launch's first entry. Phase columns: 0 / 50 / 90th percentile over the
-    busy waves, us after the launch's first entry; the last column is the
+    busy waves, us after the launch's first entry (the LayerNorm phases only
+    for cases with a LayerNorm); the last column is the
     median end of the waves of the first and of the second half of the
     workgroups (with two workgroups per CU, the first half holds one per CU).
     Prints a markdown table."""
@@ -446,7 +447,8 @@ def timeline(dev, launches=10):
     lib.svq_last_error.restype = ctypes.c_char_p
     stream = torch.cuda.Stream(dev)
     m, groups_read = 2, 512
-    stamps = torch.zeros((launches, 4096 * 4 * 8), dtype=torch.int64, device=dev)
+    slots = 12  # per wave, as the timeline build writes them
+    stamps = torch.zeros((launches, 4096 * 4 * slots), dtype=torch.int64, device=dev)
     sink = torch.empty(4096 * 256, dtype=torch.int32, device=dev)
     pool = Pool(dev, 1600 * 2**20, 160 * 2**20)
 
@@ -458,9 +460,9 @@ def timeline(dev, launches=10):
             with torch.cuda.stream(stream):
                 g.replay()
             stream.synchronize()
-        return stamps.cpu().numpy().reshape(launches, -1, 8)
+        return stamps.cpu().numpy().reshape(launches, -1, slots)
 
-    def summary(st, phases):
+    def summary(st, phases, ln=False):
         first = [w[w[:, 0] > 0][:, 0].min() for w in st]
         last = [w[w[:, 0] > 0][:, 4].max() for w in st]
         dur = statistics.median((last[i] - first[i]) / 100 for i in range(1, launches - 1))
@@ -470,16 +472,17 @@ def timeline(dev, launches=10):
         busy = w[w[:, 5] > 0] if phases else w
         pct = lambda c: "/".join(f"{v:.2f}" for v in np.percentile((busy[:, c] - t0) / 100,
                                                                    [0, 50, 90]))
-        cols = [pct(c) for c in (6, 1, 2, 3)] if phases else ["", "", "", ""]
+        lns = [pct(c) for c in (8, 9, 10)] if ln else ["", "", ""]
+        cols = ([pct(6), *lns] + [pct(c) for c in (1, 2, 3)]) if phases else [""] * 7
         ends = (st[4][:, 4] - t0) / 100
         live = st[4][:, 0] > 0
         half = np.arange(len(ends)) // 4 < live.sum() // 8  # workgroups of 4 waves
         split = "/".join(f"{np.median(ends[live & sel]):.2f}" for sel in (half, ~half))
         return [f"{dur:.2f}", f"{gap:.2f}", *cols, pct(4), split]
 
-    print("| case | qtype | launch us | gap us | x issued | x staged | step 1 | tile 1 | end | "
-          "end by half |")
-    print("|---|---|---|---|---|---|---|---|---|---|")
+    print("| case | qtype | launch us | gap us | x issued | LN mean | LN variance | LN normalized "
+          "| x staged | step 1 | tile 1 | end | end by half |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|---|---|")
     for label, qtype, n, k, fusion in TIMELINE_CASES:
         pool.reset()
         cps = pool.copies(qtype, n, k, launches)
@@ -508,7 +511,8 @@ def timeline(dev, launches=10):
                 raise RuntimeError(lib.svq_last_error().decode())
 
         print(f"| {label} | {qtype} | " + " | ".join(summary(run([lambda i=i: gemv(i) for i in
-                                                                  range(launches)]), True)) + " |")
+                                                                  range(launches)]), True,
+                                                             fusion == "ln")) + " |")
         nbytes = (cps[0][0].numel() + cps[0][1].numel() * 2) // 1024 * 1024
 
         def read(i):

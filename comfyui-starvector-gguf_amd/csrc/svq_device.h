@@ -377,6 +377,15 @@ struct XStager {
   float inv_row;  // 1 / per_row
   u32x4 v[SB];
   int dst[SB];
+#if SVQ_TIMELINE
+  // Timeline builds: this wave's stamp slots (null: no stamps).
+  unsigned long long* stamps = nullptr;
+  __device__ __forceinline__ void stamp(int slot) const {
+    if (stamps && (threadIdx.x & 63) == 0) stamps[slot] = __builtin_amdgcn_s_memrealtime();
+  }
+#else
+  __device__ __forceinline__ void stamp(int) const {}
+#endif
 
   __device__ __forceinline__ XStager(const uint16_t* x_, int k_, int cu0_, int cun_, int stride_)
       : xr(make_rsrc(x_, (uint32_t)(M * k_) * 2u)), k(k_), cu0(cu0_), cun(cun_), stride(stride_),
@@ -569,6 +578,7 @@ struct XStager {
       for (int mm = 0; mm < M; ++mm) s[mm] += valid[j] && row[j] == mm ? ps : 0.f;
     }
     block_sum(s, red1);
+    stamp(8);
 #pragma unroll
     for (int mm = 0; mm < M; ++mm) {
       mean[mm] = s[mm] / (float)k;
@@ -591,20 +601,29 @@ struct XStager {
       for (int mm = 0; mm < M; ++mm) s[mm] += valid[j] && row[j] == mm ? q : 0.f;
     }
     block_sum(s, red2);
+    stamp(9);
 #pragma unroll
     for (int mm = 0; mm < M; ++mm) rstd[mm] = 1.0f / sqrtf(s[mm] / (float)k + ln_eps);
     const int bcol = ln_cols();
     const bool unit_w = ln_w == nullptr;
+    // Every piece's parameters first (a piece past the end reads column 0's
+    // and is not stored), so the LDS reads are in flight together rather than
+    // one piece at a time behind a branch.
+    u32x4 gp[SB], bp[SB];
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
-      if (!valid[j]) continue;
+      gp[j] = lns[col[j]];
+      bp[j] = lns[bcol + col[j]];
+    }
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
       float mu = mean[0], rs = rstd[0];
 #pragma unroll
       for (int mm = 1; mm < M; ++mm) {
         mu = row[j] == mm ? mean[mm] : mu;
         rs = row[j] == mm ? rstd[mm] : rs;
       }
-      const u32x4 g = lns[col[j]], b = lns[bcol + col[j]];
+      const u32x4 g = gp[j], b = bp[j];
       const uint32_t ww[4] = {v[j].x, v[j].y, v[j].z, v[j].w}, gg[4] = {g.x, g.y, g.z, g.w},
                      bb[4] = {b.x, b.y, b.z, b.w};
       uint32_t o[4];
@@ -619,9 +638,10 @@ struct XStager {
         r.y = (_Float16)fmaf(((float)h.y - mu) * rs, g1, (float)bh.y);
         o[i] = __builtin_bit_cast(uint32_t, r);
       }
-      xs[dst[j]] = u32x4{o[0], o[1], o[2], o[3]};
+      if (valid[j]) xs[dst[j]] = u32x4{o[0], o[1], o[2], o[3]};
     }
     __syncthreads();
+    stamp(10);
   }
 
   // lns: the LDS that begin() filled with the LayerNorm parameters

@@ -50,10 +50,12 @@ struct GemvArgs {
   unsigned long long* stamps;
 };
 
-// Timeline builds: stamp slots per wave, [linear workgroup * 4 + wave][8]:
+// Timeline builds: stamp slots per wave, [linear workgroup * 4 + wave][12]:
 // 0 entry, 1 x staged, 2 first step done, 3 first tile summed, 4 end,
-// 5 tiles of the wave, 6 x loads issued, 7 work split known.
-constexpr int kTimelineSlots = 8;
+// 5 tiles of the wave, 6 x loads issued, 7 work split known; with a
+// LayerNorm staged from registers 8 mean known, 9 variance known, 10
+// normalized x in LDS; 11 unused.
+constexpr int kTimelineSlots = 12;
 constexpr int kSplitMaxSlices = 8;
 
 struct GemvShape {

@@ -291,6 +291,9 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   XStager<QT, M, WPG * 64, kStage4Batch<QT, M>, Mfma4Traits<QT>::kSxMul, LN> st(a.x, k, ubase, units,
                                                                                units);
   st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
+#if SVQ_TIMELINE
+  st.stamps = stamps_;
+#endif
   st.begin(lns);
   SVQ_STAMP(6, __builtin_amdgcn_s_memrealtime());
   uint32_t bias_bits[R];  // before the prologue: waiting for it waits for x only

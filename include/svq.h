@@ -371,11 +371,13 @@ int svq_pack_soa(const uint8_t *aos, int64_t nblocks, int qtype, uint8_t *q, uin
  * counterpart in the reference: profiling support for this library.
  *
  * svq_timeline_stamps: GEMV calls made after it (from any thread) write, for
- * every wave of the streaming MFMA kernel, 8 uint64 stamps of the 100 MHz
- * real-time clock to stamps[(linear workgroup * 4 + wave) * 8 ..]: entry,
+ * every wave of the streaming MFMA kernel, 12 uint64 stamps of the 100 MHz
+ * real-time clock to stamps[(linear workgroup * 4 + wave) * 12 ..]: entry,
  * x staged, first step done, first tile summed, end, the wave's tile count
- * (a count, not a time), x loads issued, work split known. The buffer must
- * hold 32 uint64 per workgroup of the launch; NULL stops stamping.
+ * (a count, not a time), x loads issued, work split known, and for a
+ * LayerNorm staged from registers its mean known, variance known and
+ * normalized x in LDS (else 0); the twelfth is unused. The buffer must hold
+ * 48 uint64 per workgroup of the launch; NULL stops stamping.
  *
  * svq_timeline_read: a plain coalesced read of `bytes` (a multiple of 1024,
  * below 2^31) at p by `groups` workgroups of 4 waves, stamping entry and end
