@@ -361,9 +361,7 @@ __device__ __forceinline__ float group_sum(float v, int lg_g) {
 // Split in two so that a kernel can put other loads between them: begin()
 // issues the global loads of the first SB pieces of every thread into
 // registers; finish() writes them to LDS, stages any remaining pieces in
-// batches of SB, computes the offset sums and ends with a barrier (one
-// barrier when the first batch holds all of x: the sums then come from the
-// registers). Loads
+// batches of SB, computes the offset sums and ends with a barrier. Loads
 // retire in issue order, so loads issued between begin() and finish() (the
 // weight stream) do not delay the first LDS writes. Batch entries past the end
 // re-write the last piece with the same data, so every loaded register is
@@ -463,29 +461,6 @@ struct XStager {
     load_batch(threadIdx.x);
   }
 
-  // The offset sums from pieces held in registers, when the first batch
-  // holds all of x (pcs[j]: the piece t = threadIdx.x + j * THREADS as it is
-  // stored). Piece t of row m is piece t % P of unit (t - m * per_row) / P,
-  // and per_row and THREADS are multiples of P, so the P pieces of a unit sit
-  // in P consecutive lanes: a DPP sum over the lane group gives the unit's
-  // sum, which the group's first lane stores. Every lane runs the sums (DPP
-  // reads its neighbours); entries past the end store nothing.
-  __device__ __forceinline__ void sums_from_registers(const u32x4 (&pcs)[SB], float* sxs) const {
-    static_assert(P == 2 || P == 4, "a unit is 2 or 4 pieces of 8 weights");
-    const uint32_t ones = 0x3c003c00u;  // fp16 pair (1, 1)
-#pragma unroll
-    for (int j = 0; j < SB; ++j) {
-      const int t = threadIdx.x + j * THREADS;
-      const u32x4 w = pcs[j];
-      float sx = dot2(w.w, ones, dot2(w.z, ones, dot2(w.y, ones, dot2(w.x, ones, 0.f))));
-      sx = group_sum(sx, P == 4 ? 2 : 1);
-      if (t < total && (threadIdx.x & (P - 1)) == 0) {
-        const int m = row_of(t);
-        sxs[m * stride + (t - m * per_row) / P] = sx * (T::kSxScale * SxMul);
-      }
-    }
-  }
-
   // Sum of s[] over the workgroup, left in every thread (red: one float per
   // wave and row).
   __device__ __forceinline__ void block_sum(float (&s)[M], float (*red)[M]) const {
@@ -578,9 +553,8 @@ struct XStager {
 
   // The LayerNorm when the first batch holds every piece of x (total <=
   // SB * THREADS): statistics from the registers, then only the normalized
-  // pieces are written to LDS, with their offset sums from the registers.
-  // Three barriers fewer than layer_norm() and the separate sums.
-  __device__ __forceinline__ void layer_norm_registers(u32x4* xs, const u32x4* lns, float* sxs) {
+  // pieces are written to LDS. Two barriers fewer than layer_norm().
+  __device__ __forceinline__ void layer_norm_registers(u32x4* xs, const u32x4* lns) {
     __shared__ float red1[THREADS / 64][M], red2[THREADS / 64][M];
     const uint32_t ones = 0x3c003c00u;
     int row[SB], col[SB];
@@ -635,7 +609,7 @@ struct XStager {
     // Every piece's parameters first (a piece past the end reads column 0's
     // and is not stored), so the LDS reads are in flight together rather than
     // one piece at a time behind a branch.
-    u32x4 gp[SB], bp[SB], on[SB];
+    u32x4 gp[SB], bp[SB];
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
       gp[j] = lns[col[j]];
@@ -664,10 +638,8 @@ struct XStager {
         r.y = (_Float16)fmaf(((float)h.y - mu) * rs, g1, (float)bh.y);
         o[i] = __builtin_bit_cast(uint32_t, r);
       }
-      on[j] = u32x4{o[0], o[1], o[2], o[3]};
-      if (valid[j]) xs[dst[j]] = on[j];
+      if (valid[j]) xs[dst[j]] = u32x4{o[0], o[1], o[2], o[3]};
     }
-    sums_from_registers(on, sxs);
     __syncthreads();
     stamp(10);
   }
@@ -675,23 +647,17 @@ struct XStager {
   // lns: the LDS that begin() filled with the LayerNorm parameters
   // (2 * ln_cols() pieces), used only when set_layer_norm() gave any.
   __device__ __forceinline__ void finish(u32x4* xs, float* sxs, u32x4* lns = nullptr) {
-    if (total <= SB * THREADS) {  // every piece is in registers: one barrier
-      if (LN && has_layer_norm()) {
-        layer_norm_registers(xs, lns, sxs);
-      } else {
-        store_batch(xs);
-        sums_from_registers(v, sxs);
-        __syncthreads();
-      }
-      return;
-    }
-    store_batch(xs);
-    for (int base = threadIdx.x + SB * THREADS; base < total; base += SB * THREADS) {
-      load_batch(base);
+    if (LN && has_layer_norm() && total <= SB * THREADS) {
+      layer_norm_registers(xs, lns);
+    } else {
       store_batch(xs);
+      for (int base = threadIdx.x + SB * THREADS; base < total; base += SB * THREADS) {
+        load_batch(base);
+        store_batch(xs);
+      }
+      __syncthreads();
+      if (LN && has_layer_norm()) layer_norm(xs, lns);
     }
-    __syncthreads();
-    if (LN && has_layer_norm()) layer_norm(xs, lns);
     const uint32_t ones = 0x3c003c00u;  // fp16 pair (1, 1)
     for (int t = threadIdx.x; t < M * cun; t += THREADS) {
       const int m = t / cun, u = t - m * cun;
