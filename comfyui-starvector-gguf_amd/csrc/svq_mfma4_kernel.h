@@ -298,9 +298,22 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   SVQ_STAMP(6, __builtin_amdgcn_s_memrealtime());
   uint32_t bias_bits[R];  // before the prologue: waiting for it waits for x only
   load_bias(tile_of(0), bias_bits);
+  // Weight ring steps issued before x is staged; the rest follow the staging.
+  // The x loads of the CU's other workgroup queue behind every weight load
+  // issued here. Q4_0 three-block lanes issue one step first (measured in one
+  // process at M = 2: qkv 5632 x 4608 7.7 -> 7.3 us, c_fc 18432 x 4608 13.5
+  // -> 12.8 us; 8B beam-2 decode 486 -> 494 steps/s). The other variants keep
+  // the whole ring first: one step first lost on short matrices (2304 x 2048
+  // at M = 2, Q4_0 one-unit lanes 4.9 -> 5.7 us, Q8_0 4.6 -> 5.1 us) and on
+  // the Q5_0 lm_head (31.5 -> 32.6 us). The count is a compile-time constant:
+  // with a run-time count the compiler's wait counts turn conservative and
+  // every variant lost up to 1 us.
+  constexpr int kPre = (QT == 4 && U == 3) ? 1 : D;
 #pragma unroll
-  for (int d = 0; d < D; ++d) issue(d);
+  for (int d = 0; d < kPre; ++d) issue(d);
   st.finish(xs, sxs, lns);
+#pragma unroll
+  for (int d = kPre; d < D; ++d) issue(d);
   SVQ_STAMP(1, __builtin_amdgcn_s_memrealtime());
   SVQ_STAMP(5, (unsigned long long)my_tiles);
 
