@@ -87,6 +87,9 @@ GemvArgs plan_mfma4(const GemvArgs& in, int qtype, int rows, int groups) {
   a.tiles_full = a.tile_groups - (a.tiles_hi - 1) * G;
   a.steps = (a.units + 16 * U - 1) / (16 * U);
   a.lg_ksplit = S == 4 ? 2 : S == 2 ? 1 : 0;
+  // Q5_0 three-block lanes issue one ring step before x is staged when every
+  // tile slot has at most one row tile (the kernel's SP variant).
+  a.short_prologue = qtype == 5 && U == 3 && a.tiles <= P * G;
   return a;
 }
 

@@ -45,6 +45,7 @@ struct GemvArgs {
   int tiles_full;
   int steps;        // ring steps per tile, all K ranges together
   int lg_ksplit;    // log2 of ksplit (1, 2 or 4)
+  int short_prologue;  // Q5_0 three-block lanes: one ring step before x is staged
   // Per-wave phase stamps of the streaming MFMA kernel, written only by
   // libsvq_timeline.so (built with SVQ_TIMELINE); null otherwise.
   unsigned long long* stamps;

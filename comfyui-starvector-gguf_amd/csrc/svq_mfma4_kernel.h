@@ -107,7 +107,8 @@ __device__ __forceinline__ float slot_sum(float v) {
 // 60 bytes as three 16-byte loads and one 12-byte load and its three scales as
 // 2 + 4 bytes: 6 loads per 3 units instead of 9, which the memory pipeline
 // serves about 13% faster. It needs units % 48 == 0 (K = 4608, 18432, ...).
-template <int QT, int M, int R, int D, int WPG, int U, bool LN>
+// SP (short prologue): one weight ring step before x is staged.
+template <int QT, int M, int R, int D, int WPG, int U, bool LN, bool SP = false>
 __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   static_assert(M >= 1 && M <= 8, "A has 4 rows: one half for M <= 4, two for M <= 8");
   constexpr int H = M > 4 ? 2 : 1;  // A halves (MFMA chains per unpacked B)
@@ -302,13 +303,16 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   // The x loads of the CU's other workgroup queue behind every weight load
   // issued here. Q4_0 three-block lanes issue one step first (measured in one
   // process at M = 2: qkv 5632 x 4608 7.7 -> 7.3 us, c_fc 18432 x 4608 13.5
-  // -> 12.8 us; 8B beam-2 decode 486 -> 494 steps/s). The other variants keep
-  // the whole ring first: one step first lost on short matrices (2304 x 2048
-  // at M = 2, Q4_0 one-unit lanes 4.9 -> 5.7 us, Q8_0 4.6 -> 5.1 us) and on
-  // the Q5_0 lm_head (31.5 -> 32.6 us). The count is a compile-time constant:
-  // with a run-time count the compiler's wait counts turn conservative and
-  // every variant lost up to 1 us.
-  constexpr int kPre = (QT == 4 && U == 3) ? 1 : D;
+  // -> 12.8 us; 8B beam-2 decode 486 -> 494 steps/s), and so do Q5_0 ones
+  // with SP, which the host sets when every tile slot has at most one row
+  // tile (qkv 8.8 -> 8.1 us, o_proj 8.3 -> 7.8 us; with more tiles per slot
+  // one step first lost: c_fc 15.6 -> 15.8, c_proj's slices 18.8 -> 19.1,
+  // lm_head 31.5 -> 32.6 us). The other variants keep the whole ring
+  // first: one step first lost on short matrices (2304 x 2048 at M = 2,
+  // Q4_0 one-unit lanes 4.9 -> 5.7 us, Q8_0 4.6 -> 5.1 us). The count is a
+  // compile-time constant: with a run-time count the compiler's wait counts
+  // turn conservative and every variant lost up to 1 us.
+  constexpr int kPre = (SP || (QT == 4 && U == 3)) ? 1 : D;
 #pragma unroll
   for (int d = 0; d < kPre; ++d) issue(d);
   st.finish(xs, sxs, lns);
@@ -451,30 +455,32 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   SVQ_STAMP(4, __builtin_amdgcn_s_memrealtime());
 }
 
-template <int QT, int M, int R, int D, int U, bool LN>
+template <int QT, int M, int R, int D, int U, bool LN, bool SP>
 const void* mfma4_kernel_ptr() {
-  return reinterpret_cast<const void*>(&gemv_mfma4_kernel<QT, M, R, D, kStreamWavesPerGroup, U, LN>);
+  return reinterpret_cast<const void*>(
+      &gemv_mfma4_kernel<QT, M, R, D, kStreamWavesPerGroup, U, LN, SP>);
 }
 
-template <int QT, int M, int R, int D, int U, bool LN>
+template <int QT, int M, int R, int D, int U, bool LN, bool SP>
 hipError_t mfma4_launch(const GemvArgs& a, int groups, size_t lds, hipStream_t stream) {
   // groups = K slices (gridDim.x) x workgroups per slice (gridDim.y).
   const int sl = a.partial ? a.slices : 1;
-  hipLaunchKernelGGL((gemv_mfma4_kernel<QT, M, R, D, kStreamWavesPerGroup, U, LN>),
+  hipLaunchKernelGGL((gemv_mfma4_kernel<QT, M, R, D, kStreamWavesPerGroup, U, LN, SP>),
                      dim3(sl, groups / sl), dim3(kStreamWavesPerGroup * 64), lds, stream, a);
   return hipGetLastError();
 }
 
 // One (R, D, U) variant, with or without the LayerNorm staging.
-template <int QT, int M, int R, int D, int U>
+template <int QT, int M, int R, int D, int U, bool SP = false>
 hipError_t mfma4_variant(const GemvArgs& a, bool ln, int groups, size_t lds, hipStream_t stream,
                          const void** fn) {
   if (fn) {
-    *fn = ln ? mfma4_kernel_ptr<QT, M, R, D, U, true>() : mfma4_kernel_ptr<QT, M, R, D, U, false>();
+    *fn = ln ? mfma4_kernel_ptr<QT, M, R, D, U, true, SP>()
+             : mfma4_kernel_ptr<QT, M, R, D, U, false, SP>();
     return hipSuccess;
   }
-  return ln ? mfma4_launch<QT, M, R, D, U, true>(a, groups, lds, stream)
-            : mfma4_launch<QT, M, R, D, U, false>(a, groups, lds, stream);
+  return ln ? mfma4_launch<QT, M, R, D, U, true, SP>(a, groups, lds, stream)
+            : mfma4_launch<QT, M, R, D, U, false, SP>(a, groups, lds, stream);
 }
 
 // rows 1: one row set per lane with an 8-deep ring; rows 2: two row sets
@@ -486,6 +492,9 @@ hipError_t mfma4_dispatch_r(const GemvArgs& a, bool ln, int rows, int groups, si
                             hipStream_t stream, const void** fn) {
   if (rows == 3) {
     if constexpr (QT == 8) return mfma4_variant<QT, M, 1, 4, 2>(a, ln, groups, lds, stream, fn);
+    else if constexpr (QT == 5)
+      return a.short_prologue ? mfma4_variant<QT, M, 1, 3, 3, true>(a, ln, groups, lds, stream, fn)
+                              : mfma4_variant<QT, M, 1, 3, 3>(a, ln, groups, lds, stream, fn);
     else return mfma4_variant<QT, M, 1, 3, 3>(a, ln, groups, lds, stream, fn);
   }
   if (rows == 2) return mfma4_variant<QT, M, 2, 4, 1>(a, ln, groups, lds, stream, fn);
