@@ -143,7 +143,8 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   // for x does not wait for the weights, while the weight stream starts one
   // cache round trip earlier than if x were staged completely first. (x loads
   // issued behind the prologue would wait for the whole chip-wide prologue
-  // burst.) Pieces beyond the first batch are staged after the prologue.
+  // burst.) Pieces beyond the first batch are staged before the ring steps
+  // that follow the staging.
   XStager<QT, M, WPG * 64, kStageBatch<QT, M>, 1, LN> st(a.x, k, 0, units, units);
   st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
   st.begin(lns);
