@@ -307,12 +307,16 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   // with SP, which the host sets when every tile slot has at most one row
   // tile (qkv 8.8 -> 8.1 us, o_proj 8.3 -> 7.8 us; with more tiles per slot
   // one step first lost: c_fc 15.6 -> 15.8, c_proj's slices 18.8 -> 19.1,
-  // lm_head 31.5 -> 32.6 us). The other variants keep the whole ring
-  // first: one step first lost on short matrices (2304 x 2048 at M = 2,
-  // Q4_0 one-unit lanes 4.9 -> 5.7 us, Q8_0 4.6 -> 5.1 us). The count is a
-  // compile-time constant: with a run-time count the compiler's wait counts
-  // turn conservative and every variant lost up to 1 us.
-  constexpr int kPre = (SP || (QT == 4 && U == 3)) ? 1 : D;
+  // lm_head 31.5 -> 32.6 us). One-unit lanes and Q8_0 whole-block lanes
+  // issue half their ring first (one step first lost on short matrices:
+  // 2304 x 2048 at M = 2, Q4_0 4.9 -> 5.7 us, Q8_0 4.6 -> 5.1 us; half the
+  // ring gains up to 0.6 us at K = 2048 and 8192, e.g. Q4_0 49152 x 2048 at
+  // M = 2 14.5 -> 13.9 us, Q5_0 2048 x 8192 8.2 -> 7.7 us, and loses at most
+  // 0.4 us). Q5_0 three-block lanes without SP keep the whole ring first.
+  // The count is a compile-time constant: with a run-time count the
+  // compiler's wait counts turn conservative and every variant lost up to
+  // 1 us.
+  constexpr int kPre = (SP || (QT == 4 && U == 3)) ? 1 : U == 3 ? D : D / 2;
 #pragma unroll
   for (int d = 0; d < kPre; ++d) issue(d);
   st.finish(xs, sxs, lns);
