@@ -14,20 +14,28 @@ namespace {
 // the first is used: one memory round trip instead of one per load.
 __global__ __launch_bounds__(256) void split_finish_kernel(GemvArgs a, int m_rows,
                                                            float out_scale) {
+  // The arguments the loads need, in scalar registers before the first
+  // branch: one scalar memory round trip at entry.
+  int n = a.n, slices = a.slices, y_f32 = a.y_f32;
+  const float* partial = a.partial;
+  const uint16_t* bias_p = a.bias;
+  const uint16_t* residual = a.residual;
+  asm volatile("" : "+s"(n), "+s"(slices), "+s"(y_f32), "+s"(partial), "+s"(bias_p),
+                    "+s"(residual));
   const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= m_rows * a.n) return;
-  const int m = i / a.n, row = i - m * a.n;
+  if (i >= m_rows * n) return;
+  const int m = i / n, row = i - m * n;
   float p[kSplitMaxSlices];
 #pragma unroll
   for (int sl = 0; sl < kSplitMaxSlices; ++sl)
-    p[sl] = sl < a.slices ? a.partial[((size_t)sl * m_rows + m) * a.n + row] : 0.f;
-  const uint16_t bias = a.bias ? a.bias[row] : 0;
-  const uint16_t res = a.residual && !a.y_f32 ? a.residual[i] : 0;
+    p[sl] = sl < slices ? partial[((size_t)sl * m_rows + m) * n + row] : 0.f;
+  const uint16_t bias = bias_p ? bias_p[row] : 0;
+  const uint16_t res = residual && !y_f32 ? residual[i] : 0;
   float v = 0.f;
 #pragma unroll
   for (int sl = 0; sl < kSplitMaxSlices; ++sl)
-    if (sl < a.slices) v += p[sl];
-  const float b = a.bias ? half_bits_to_float(bias) : 0.f;
+    if (sl < slices) v += p[sl];
+  const float b = bias_p ? half_bits_to_float(bias) : 0.f;
   store_y_loaded(a, i, __builtin_fmaf(v, out_scale, b), res);
 }
 

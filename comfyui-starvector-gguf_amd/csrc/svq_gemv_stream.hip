@@ -49,10 +49,21 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   constexpr int XW = T::kUnitWeights / 2;  // activation dwords per unit
   extern __shared__ u32x4 lds[];
 
-  const int n = a.n, k = a.k;
+  // Every argument the work split and the first loads need, pinned in
+  // scalar registers before the first branch (one scalar memory round trip
+  // at entry instead of one per branch on the way to the first x load).
+  int n = a.n, k = a.k, lg_g = a.lg_g, W = a.waves, grid_x = (int)gridDim.x;
+  const uint16_t* a_x = a.x;
+  const uint8_t* a_q = a.q;
+  const uint16_t* a_s = a.s;
+  const uint16_t* a_bias = a.bias;
+  const uint16_t* a_ln_w = LN ? a.ln_w : nullptr;
+  const uint16_t* a_ln_b = LN ? a.ln_b : nullptr;
+  asm volatile(""
+               : "+s"(n), "+s"(k), "+s"(lg_g), "+s"(W), "+s"(grid_x), "+s"(a_x), "+s"(a_q),
+                 "+s"(a_s), "+s"(a_bias), "+s"(a_ln_w), "+s"(a_ln_b));
   const int kb = k >> 5;
   const int units = kb * T::kUnitsPerBlock;
-  const int lg_g = a.lg_g;
   const int G = 1 << lg_g;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -60,13 +71,12 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   const int rg = lane >> lg_g;
   const int tile_rows = (64 >> lg_g) * R;
   const int tiles = (n + tile_rows - 1) / tile_rows;
-  const int W = a.waves;
   // At most one tile per wave: wave-major numbering (wave w of workgroup b
   // is wid = w * gridDim.x + b), which spreads the idle waves of a short
   // matrix over all workgroups, hence over all CUs. Otherwise wid =
   // b * WPG + w: the waves of a workgroup stream neighbouring tiles.
   const bool wave_major = tiles <= W;
-  const int wid = wave_major ? wave * (int)gridDim.x + (int)blockIdx.x
+  const int wid = wave_major ? wave * grid_x + (int)blockIdx.x
                              : (int)blockIdx.x * WPG + wave;
   const int my_tiles = wid < W ? (tiles - wid + W - 1) / W : 0;
   const int niter = (units + G - 1) >> lg_g;  // unit iterations per tile
@@ -78,16 +88,16 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
 
   // Buffer resources over the whole arrays (the C ABI keeps them < 2^31
   // bytes); a missing bias is a zero-length range, so its loads read zeros.
-  const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)n * row_bytes);
-  const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)n * (uint32_t)kb * 2u);
-  const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bias, a.bias ? (uint32_t)n * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(a_q, (uint32_t)n * row_bytes);
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(a_s, (uint32_t)n * (uint32_t)kb * 2u);
+  const __amdgpu_buffer_rsrc_t br = make_rsrc(a_bias, a_bias ? (uint32_t)n * 2u : 0u);
 
   // Static LDS: the Q5_0 mask table (a compile-time address, so lookups
   // need no base register). Dynamic LDS: x pieces, then offset sums.
   __shared__ u32x2 q5_table[QT == 5 ? 256 : 1];
   if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
   // LDS: x pieces, LayerNorm parameters (if any), offset sums.
-  const bool ln = LN && (a.ln_w || a.ln_b);
+  const bool ln = LN && (a_ln_w || a_ln_b);
   u32x4* xs = lds;
   u32x4* lns = xs + M * P * units;
   float* sxs = reinterpret_cast<float*>(lns + (ln ? 2 * ((k / 8 + 63) / 64 * 64) : 0));
@@ -145,8 +155,8 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   // issued behind the prologue would wait for the whole chip-wide prologue
   // burst.) Pieces beyond the first batch are staged before the ring steps
   // that follow the staging.
-  XStager<QT, M, WPG * 64, kStageBatch<QT, M>, 1, LN> st(a.x, k, 0, units, units);
-  st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
+  XStager<QT, M, WPG * 64, kStageBatch<QT, M>, 1, LN> st(a_x, k, 0, units, units);
+  st.set_layer_norm(a_ln_w, a_ln_b, a.ln_eps);
   st.begin(lns);
   // An 8-deep ring issues half its steps before x is staged and the rest
   // after: the x loads of the CU's other workgroup then queue behind fewer

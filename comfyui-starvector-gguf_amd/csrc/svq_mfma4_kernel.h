@@ -127,16 +127,34 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
                                 kTimelineSlots
                : nullptr;
 #endif
-  const int n = a.n, k = a.k;
+  // Every argument the work split and the first loads need, pinned in
+  // scalar registers before the first branch: the compiler otherwise loads
+  // each one just ahead of its first use, behind the branches, one scalar
+  // memory round trip per branch on the way to the first x load.
+  int n = a.n, k = a.k, a_units = a.units, a_tiles = a.tiles, a_groups = a.tile_groups;
+  int a_wave_major = a.wave_major, a_tiles_hi = a.tiles_hi, a_tiles_full = a.tiles_full;
+  int a_steps = a.steps, a_lg_ksplit = a.lg_ksplit;
+  int grid_x = (int)gridDim.x, grid_y = (int)gridDim.y;
+  const uint16_t* a_x = a.x;
+  const uint8_t* a_q = a.q;
+  const uint16_t* a_s = a.s;
+  const uint16_t* a_bias = a.bias;
+  const uint16_t* a_ln_w = LN ? a.ln_w : nullptr;
+  const uint16_t* a_ln_b = LN ? a.ln_b : nullptr;
+  asm volatile(""
+               : "+s"(n), "+s"(k), "+s"(a_units), "+s"(a_tiles), "+s"(a_groups),
+                 "+s"(a_wave_major), "+s"(a_tiles_hi), "+s"(a_tiles_full), "+s"(a_steps),
+                 "+s"(a_lg_ksplit), "+s"(grid_x), "+s"(grid_y), "+s"(a_x), "+s"(a_q),
+                 "+s"(a_s), "+s"(a_bias), "+s"(a_ln_w), "+s"(a_ln_b));
   const int kb = k >> 5;
   // K slices across workgroups (a.partial set, gridDim.x = a.slices >= 2):
   // workgroup (slice, b) takes that slice of every row -- units ubase ..
   // ubase + units, x staged for that slice only -- and writes raw partial
   // sums. Otherwise one slice: the whole row. The slices of a row set are
   // consecutive in dispatch order.
-  const int SL = (int)gridDim.x;
+  const int SL = grid_x;
   const int slice = (int)blockIdx.x;
-  const int units = a.units;
+  const int units = a_units;
   const int ubase = slice * units;
   const int bx = (int)blockIdx.y;  // workgroup within its slice
   const int lane = threadIdx.x & 63;
@@ -150,12 +168,12 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   // wave (p, sk) streams steps [st0, st1) of each tile of slot p. With S > 1
   // workgroup g processes tile groups g, g + G, ... (P tiles each) and the S
   // partial sums of a tile meet in LDS at the end of its group.
-  const int lg_s = a.lg_ksplit, S = 1 << lg_s, P = WPG >> lg_s;
+  const int lg_s = a_lg_ksplit, S = 1 << lg_s, P = WPG >> lg_s;
   const int p_id = wave >> lg_s, sk = wave & (S - 1);
   const int tile_rows = 4 * R;
-  const int tiles = a.tiles;
-  const int groups = a.tile_groups;
-  const int G = (int)gridDim.y;
+  const int tiles = a_tiles;
+  const int groups = a_groups;
+  const int G = grid_y;
   // At most one tile per wave (S = 1): wave-major tiles (wave p of
   // workgroup g owns tile wv = p * G + g), which spreads the idle waves of a
   // short matrix over all workgroups, hence over all CUs. Otherwise workgroup
@@ -164,13 +182,13 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   // of a tile slot meet at a barrier per tile, so every wave of a workgroup
   // walks the same number of tile groups.
   const int WV = P * G;
-  const bool wave_major = a.wave_major != 0;
+  const bool wave_major = a_wave_major != 0;
   const int wv = p_id * G + bx;
   // Tile groups bx, bx + G, ... below `groups`: tiles_hi of them for
   // workgroups below tiles_full, one fewer from there (none past groups).
   const int my_tiles = wave_major ? (wv < tiles ? 1 : 0)
-                                  : (bx < a.tiles_full ? a.tiles_hi : a.tiles_hi - 1);
-  const int niter_all = a.steps;
+                                  : (bx < a_tiles_full ? a_tiles_hi : a_tiles_hi - 1);
+  const int niter_all = a_steps;
   const int st0 = (sk * niter_all) >> lg_s, st1 = ((sk + 1) * niter_all) >> lg_s;
   const int steps = my_tiles * (st1 - st0);
   auto tile_of = [&](int j) { return wave_major ? wv + j * WV : (bx + j * G) * P + p_id; };
@@ -185,14 +203,14 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   if (bx >= (wave_major ? tiles : groups)) return;
   const uint32_t row_bytes = (uint32_t)kb * T::kBlockQ;
 
-  const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)n * row_bytes);
-  const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)n * (uint32_t)kb * 2u);
-  const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bias, a.bias ? (uint32_t)n * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(a_q, (uint32_t)n * row_bytes);
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(a_s, (uint32_t)n * (uint32_t)kb * 2u);
+  const __amdgpu_buffer_rsrc_t br = make_rsrc(a_bias, a_bias ? (uint32_t)n * 2u : 0u);
 
   if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
   constexpr int XP = T::kUnitWeights / 8;  // 16-byte x pieces per unit
   // LDS: x pieces, LayerNorm parameters (if any), offset sums, split-K sums.
-  const bool ln = LN && (a.ln_w || a.ln_b);
+  const bool ln = LN && (a_ln_w || a_ln_b);
   u32x4* xs = lds;
   u32x4* lns = xs + M * XP * units;
   float* sxs = reinterpret_cast<float*>(lns + (ln ? 2 * ((k / 8 + 63) / 64 * 64) : 0));
@@ -289,9 +307,9 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
 
   // x and bias loads first, then the weight prologue, then x is written to
   // LDS (vector loads retire in issue order).
-  XStager<QT, M, WPG * 64, kStage4Batch<QT, M>, Mfma4Traits<QT>::kSxMul, LN> st(a.x, k, ubase, units,
+  XStager<QT, M, WPG * 64, kStage4Batch<QT, M>, Mfma4Traits<QT>::kSxMul, LN> st(a_x, k, ubase, units,
                                                                                units);
-  st.set_layer_norm(a.ln_w, a.ln_b, a.ln_eps);
+  st.set_layer_norm(a_ln_w, a_ln_b, a.ln_eps);
 #if SVQ_TIMELINE
   st.stamps = stamps_;
 #endif
