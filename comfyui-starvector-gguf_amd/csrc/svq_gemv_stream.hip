@@ -95,7 +95,6 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   // Static LDS: the Q5_0 mask table (a compile-time address, so lookups
   // need no base register). Dynamic LDS: x pieces, then offset sums.
   __shared__ u32x2 q5_table[QT == 5 ? 256 : 1];
-  if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
   // LDS: x pieces, LayerNorm parameters (if any), offset sums.
   const bool ln = LN && (a_ln_w || a_ln_b);
   u32x4* xs = lds;
@@ -168,6 +167,9 @@ __global__ __launch_bounds__(WPG * 64) void gemv_stream_kernel(GemvArgs a) {
   for (int d = 0; d < kPre; ++d) issue(d);
   uint32_t bias_bits[R];
   load_bias(wid, bias_bits);
+  // The fifth-bit table is built while x is in flight; the staging's
+  // barrier orders its LDS writes before the first lookup.
+  if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
   st.finish(xs, sxs, lns);
 #pragma unroll
   for (int d = kPre; d < D; ++d) issue(d);

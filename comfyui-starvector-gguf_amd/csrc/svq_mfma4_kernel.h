@@ -207,7 +207,6 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(a_s, (uint32_t)n * (uint32_t)kb * 2u);
   const __amdgpu_buffer_rsrc_t br = make_rsrc(a_bias, a_bias ? (uint32_t)n * 2u : 0u);
 
-  if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
   constexpr int XP = T::kUnitWeights / 8;  // 16-byte x pieces per unit
   // LDS: x pieces, LayerNorm parameters (if any), offset sums, split-K sums.
   const bool ln = LN && (a_ln_w || a_ln_b);
@@ -317,6 +316,9 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   SVQ_STAMP(6, __builtin_amdgcn_s_memrealtime());
   uint32_t bias_bits[R];  // before the prologue: waiting for it waits for x only
   load_bias(tile_of(0), bias_bits);
+  // The fifth-bit table is built while x is in flight; the staging's
+  // barrier orders its LDS writes before the first lookup.
+  if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
   // Weight ring steps issued before x is staged; the rest follow the staging.
   // The x loads of the CU's other workgroup queue behind every weight load
   // issued here. Q4_0 three-block lanes issue one step first (measured in one
