@@ -259,9 +259,9 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
   // 8B shapes against the 16x16x32 kernel: faster for Q5_0 and Q8_0 at every
   // M (Q5_0 c_fc 39.1 -> 22.6 us, Q8_0 lm_head 94.8 -> 51.0 us at M = 5; at M
   // = 8 Q5_0 c_fc 31.0 -> 26.6 us, lm_head 52.1 -> 45.3 us, Q8_0 lm_head 75.8
-  // -> 65.1 us) and for Q4_0 at M = 5..6; Q4_0 at M = 7..8 is 1-2 us faster
-  // on the 16x16x32 kernel (lm_head 39.9 against 43.6 us at M = 8).
-  if (tu.path == 0 && m >= 7 && qtype == SVQ_Q4_0) return false;
+  // -> 65.1 us) and for Q4_0 at every M (at M = 8: c_fc 24.5 -> 21.5 us,
+  // lm_head 40.2 -> 36.8 us, qkv 13.0 -> 12.2 us, 2048 x 8192 13.4 -> 13.5
+  // us with one row set).
   // Automatic choice (measured at the StarCoder2-8B and GPTBigCode-1B shapes):
   // the matrix-core path wins for Q5_0 at every M and for Q4_0 / Q8_0 from
   // M = 2; at M = 1 the vector path's dot products are cheap enough, except
@@ -325,8 +325,14 @@ bool choose_mfma4(int m, int n, int k, int qtype, const Tuning& tu, int* rows_ou
     const int tile_rows = rows == 2 ? 8 : 4;
     tiles = (n + tile_rows - 1) / tile_rows;
     // Two row sets per lane share each x read; measured faster down to an
-    // eighth of the resident waves (Q4_0 / Q8_0 at K = 4608, M = 2..4).
-    if (tiles >= wmax || rows != 2 || tu.mfma_r || 8 * (int64_t)tiles >= wmax) break;
+    // eighth of the resident waves (Q4_0 / Q8_0 at K = 4608, M = 2..4), and
+    // for Q4_0 at M = 7..8 above a quarter (at M = 8: 2048 x 8192, a quarter
+    // exactly, one row set 13.6 against 15.5 us; 2304 x 2048 6.9 against 7.9
+    // us; 4608 x 4608 two row sets 12.1 against 13.9 us; at M = 5 the
+    // quarter rule put 4608 x 4608 on one row set, 11.4 against 10.8 us).
+    const bool keep_two = qtype == SVQ_Q4_0 && m >= 7 ? 4 * (int64_t)tiles > wmax
+                                                       : 8 * (int64_t)tiles >= wmax;
+    if (tiles >= wmax || rows != 2 || tu.mfma_r || keep_two) break;
     rows = 1;
   }
   // Long rows with too few tiles to fill the GPU go to the vector kernel,
