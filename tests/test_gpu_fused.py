@@ -86,6 +86,7 @@ def torch_ref(c, ln=False, ln_bias=True, res=False, gelu=False, eps=1e-5):
 
 SHAPES = [
     (2, 5632, 4608, "Q4_0"),   # 8B fused q/k/v at beam 2
+    (2, 5632, 4608, "Q5_0"),   # Q5_0 q/k/v: one row tile per tile slot, short prologue
     (2, 4608, 18432, "Q5_0"),  # 8B c_proj: K = 18432 staged in LDS
     (1, 1000, 4608, "Q8_0"),
     (4, 300, 2048, "Q5_0"),
