@@ -15,20 +15,31 @@ namespace {
 __global__ __launch_bounds__(256) void split_finish_kernel(GemvArgs a, int m_rows,
                                                            float out_scale) {
   // The arguments the loads need, in scalar registers before the first
-  // branch: one scalar memory round trip at entry.
+  // branch: one scalar memory round trip at entry. The pointers come back
+  // from the asm as plain pointers; the casts restore the global address
+  // space, so the loads stay global loads (not flat ones, which also count
+  // against the LDS wait counter).
+  typedef __attribute__((address_space(1))) const float gfloat;
+  typedef __attribute__((address_space(1))) const uint16_t gu16;
   int n = a.n, slices = a.slices, y_f32 = a.y_f32;
-  const float* partial = a.partial;
-  const uint16_t* bias_p = a.bias;
-  const uint16_t* residual = a.residual;
-  asm volatile("" : "+s"(n), "+s"(slices), "+s"(y_f32), "+s"(partial), "+s"(bias_p),
-                    "+s"(residual));
+  const float* partial_p = a.partial;
+  const uint16_t* bias_pp = a.bias;
+  const uint16_t* residual_p = a.residual;
+  asm volatile("" : "+s"(n), "+s"(slices), "+s"(y_f32), "+s"(partial_p), "+s"(bias_pp),
+                    "+s"(residual_p));
+  gfloat* partial = (gfloat*)partial_p;
+  gu16* bias_p = (gu16*)bias_pp;
+  gu16* residual = (gu16*)residual_p;
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= m_rows * n) return;
   const int m = i / n, row = i - m * n;
+  // Every slot's load unconditionally (slots past `slices` re-read slice
+  // 0), so all of them are in flight together: a load behind a branch is
+  // waited for before the next branch.
   float p[kSplitMaxSlices];
 #pragma unroll
   for (int sl = 0; sl < kSplitMaxSlices; ++sl)
-    p[sl] = sl < slices ? partial[((size_t)sl * m_rows + m) * n + row] : 0.f;
+    p[sl] = partial[((size_t)(sl < slices ? sl : 0) * m_rows + m) * n + row];
   const uint16_t bias = bias_p ? bias_p[row] : 0;
   const uint16_t res = residual && !y_f32 ? residual[i] : 0;
   float v = 0.f;
