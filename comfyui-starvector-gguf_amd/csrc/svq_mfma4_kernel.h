@@ -320,7 +320,11 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   // beam-2 decode 508 -> 518 steps/s, 1B 990 -> 1000 (the loads alone: 514
   // and 996; priority 1 and 3 alike). Raised from the x loads through the
   // finish, weight prologue included: step 75.4 us, but 8B decode 510 and 1B
-  // 975 steps/s.
+  // 975 steps/s (both decoders are Q4_0), so only Q5_0 keeps the raise over
+  // its weight prologue (against dropping it there: qkv 5632 x 4608 7.74 ->
+  // 7.47 us, o_proj 7.31 -> 7.12 us, step 76.2 -> 75.7 us; Q4_0 and Q8_0
+  // shapes and both decoders unchanged).
+  constexpr bool kRaisedPrologue = QT == 5;
   __builtin_amdgcn_s_setprio(1);
   st.begin(lns);
   SVQ_STAMP(6, __builtin_amdgcn_s_memrealtime());
@@ -329,7 +333,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   // The fifth-bit table is built while x is in flight; the staging's
   // barrier orders its LDS writes before the first lookup.
   if constexpr (QT == 5) build_q5_table(q5_table, threadIdx.x, WPG * 64);
-  __builtin_amdgcn_s_setprio(0);
+  if constexpr (!kRaisedPrologue) __builtin_amdgcn_s_setprio(0);
   // Weight ring steps issued before x is staged; the rest follow the staging.
   // The x loads of the CU's other workgroup queue behind every weight load
   // issued here. Q4_0 three-block lanes issue one step first (measured in one
@@ -350,7 +354,7 @@ __global__ __launch_bounds__(WPG * 64) void gemv_mfma4_kernel(GemvArgs a) {
   constexpr int kPre = (SP || (QT == 4 && U == 3)) ? 1 : U == 3 ? D : D / 2;
 #pragma unroll
   for (int d = 0; d < kPre; ++d) issue(d);
-  __builtin_amdgcn_s_setprio(1);
+  if constexpr (!kRaisedPrologue) __builtin_amdgcn_s_setprio(1);
   st.finish(xs, sxs, lns);
   __builtin_amdgcn_s_setprio(0);
 #pragma unroll
