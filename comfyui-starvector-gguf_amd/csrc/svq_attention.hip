@@ -39,7 +39,8 @@ constexpr int kD = 128;                        // head dimension
 // the same span (208 instead of 104 at beam 2, 4 kv heads, span 1537), with a
 // shorter cross-wave reduction and twice the partials to merge. Measured in
 // one process against four waves: 8B beam-2 decode 517 -> 524 steps/s,
-// GPTBigCode-1B 1003 -> 1019; one wave (32-slot chunks): 510 and 997.
+// GPTBigCode-1B 1003 -> 1019; one wave (32-slot chunks): 510 and 997;
+// three waves: 520 and 1001.
 constexpr int kWaves = 2;
 constexpr int kChunk = kWaves * 32;            // slots per workgroup (32 per wave)
 constexpr uint32_t kOutOfRange = 0x80000000u;  // past every buffer range
