@@ -188,9 +188,10 @@ def test_decode_attention_rejects_bad_arguments(kw, code):
 
 def test_decode_attention_workspace_size():
     lib = native.load()
-    # Per (row, query head) and chunk of 128 slots: (max, sum) as 8 bytes,
-    # padded to 256 bytes in all, then 128 fp32 weighted-V sums.
-    assert lib.svq_decode_attention_workspace(2, 36, 4, 1537) == 7680 + 2 * 36 * 13 * 512
+    # Per (row, query head) and chunk of 64 slots (25 for span 1537): (max,
+    # sum) as 8 bytes, padded to 256 bytes in all, then 128 fp32 weighted-V
+    # sums.
+    assert lib.svq_decode_attention_workspace(2, 36, 4, 1537) == 14592 + 2 * 36 * 25 * 512
     assert lib.svq_decode_attention_workspace(2, 16, 1, 64) == 256 + 2 * 16 * 512
     assert lib.svq_decode_attention_workspace(2, 36, 5, 64) == -2
     assert lib.svq_decode_attention_workspace(2, 34, 2, 64) == -2  # 17 heads per kv head
